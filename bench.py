@@ -1,0 +1,219 @@
+"""Benchmark of the MI355X paged-decode hot path: K/V write + batched GQA paged attention.
+
+One step = write every sequence's newest K/V row into its block, then one
+batched paged-attention call over the whole batch (the per-layer work of a
+decode step, reference engine/kernels/paged_attention_integration.py:148-171).
+
+Default workload (the headline configuration): batch 256, 14 q / 2 kv heads,
+head_dim 64, block 16, fp16, lengths lognormal (median 4096, sigma 0.5) clipped
+to [256, 32768], groups of 8 sequences sharing their first 64 blocks. Inputs are
+synthetic N(0, 1) data resident in HBM before timing starts. R copies of the
+pool are rotated so that no step finds the previous step's data in the 256 MB
+MALL (Infinity Cache).
+
+Output: one JSON line. value = algorithmic bytes of one attention call (K/V at
+the distinct token slots read, Q, O, table entries, lengths) / mean duration of
+the attention call measured with HIP events on the launch stream.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+REPO_ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(REPO_ROOT))
+sys.path.insert(0, str(REPO_ROOT / "vllm-inference-engine_amd"))
+
+HBM_PEAK_GBS = 8000.0
+TRAFFIC_SUMMARY = REPO_ROOT / "profiles" / "long_context_traffic.md"
+
+
+def parse_args():
+    p = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=50)
+    p.add_argument("--warmup", type=int, default=10)
+    p.add_argument("--workload", default="long_context",
+                   help="long_context | gqa_sweep_kv{28,14,7,4} | qwen_layer | softmax_stress")
+    p.add_argument("--copies", type=int, default=4, help="rotated pool copies (cache defeat)")
+    p.add_argument("--seed", type=int, default=0)
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--cpu-seconds", type=float, default=15.0,
+                   help="approximate CPU time budget of the oracle baseline sample")
+    return p.parse_args()
+
+
+def make_workload(name, device, seed):
+    from engine import workloads
+
+    if name == "long_context":
+        return workloads.long_context(device=device, seed=seed)
+    if name.startswith("gqa_sweep_kv"):
+        return workloads.gqa_sweep(int(name[len("gqa_sweep_kv"):]), device=device, seed=seed)
+    if name == "qwen_layer":
+        return workloads.qwen_layer(device=device, seed=seed)
+    if name == "softmax_stress":
+        return workloads.softmax_stress(device=device, seed=seed)
+    raise SystemExit(f"unknown workload {name}")
+
+
+def read_traffic():
+    """HBM bytes per launch from the committed rocprofv3 --pmc summary, if present."""
+    if not TRAFFIC_SUMMARY.exists():
+        return None
+    for line in TRAFFIC_SUMMARY.read_text().splitlines():
+        if line.startswith("traffic_bytes_per_launch:"):
+            try:
+                return int(float(line.split(":", 1)[1].strip()))
+            except ValueError:
+                return None
+    return None
+
+
+def cpu_baseline(w, budget_s):
+    """The oracle's literal fp16 path (the reference's CPU PyTorch algorithm) on a sample."""
+    import torch
+
+    from engine import workloads
+    from oracle.paged_attention_oracle import naive_reference_paged_attention
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    order = list(range(w.num_seqs))
+    done, t_total, nbytes = [], 0.0, 0
+    bs = w.k_cache.shape[1]
+    hkv, d = w.k_cache.shape[2], w.k_cache.shape[3]
+    hq = w.q.shape[1]
+    for i in order:
+        q, k, v, tables, lens = workloads.gather_subset(w, [i])
+        t0 = time.perf_counter()
+        naive_reference_paged_attention(q, k, v, tables, lens, w.scale)
+        t_total += time.perf_counter() - t0
+        done.append(i)
+        n = lens[0]
+        nbytes += 2 * hkv * d * 2 * n + 2 * hq * d * 2 + 4 * ((n + bs - 1) // bs) + 4
+        if t_total >= budget_s:
+            break
+    return {
+        "value": round(nbytes / t_total / 1e9, 4),
+        "unit": "GB/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": (f"oracle literal fp16 path (per-sequence gather + einsum + softmax) over "
+                   f"{len(done)} of {w.num_seqs} sequences ({sum(w.lens[i] for i in done)} tokens), "
+                   f"{t_total:.1f} s; per-sequence bytes counted without prefix sharing"),
+    }
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build measures one GPU; --gpus must be 1 "
+                          "(the path would shard by sequence or kv head, see DESIGN.md)"}))
+        raise SystemExit(2)
+    import torch
+
+    from engine.kernels.paged_attention import paged_attention_decode_batched
+    from engine.kernels.paged_attention_integration import paged_kv_write
+
+    dev = torch.device("cuda", 0)
+    copies = [make_workload(args.workload, dev, args.seed)]
+    base = copies[0]
+    for _ in range(1, max(1, args.copies)):
+        from engine.workloads import Workload
+
+        copies.append(Workload(name=base.name, q=base.q.clone(), k_cache=base.k_cache.clone(),
+                               v_cache=base.v_cache.clone(), block_tables=base.block_tables.clone(),
+                               seq_lens=base.seq_lens.clone(), tables=base.tables, lens=base.lens,
+                               scale=base.scale, unique_slots=base.unique_slots, meta=base.meta))
+    g = torch.Generator(device=dev).manual_seed(args.seed + 7)
+    hkv, d = base.k_cache.shape[2], base.k_cache.shape[3]
+    new_k = torch.randn(base.num_seqs, hkv, d, generator=g, device=dev).half()
+    new_v = torch.randn(base.num_seqs, hkv, d, generator=g, device=dev).half()
+
+    def step(i, ev=None):
+        w = copies[i % len(copies)]
+        paged_kv_write(new_k, new_v, w.k_cache, w.v_cache, w.block_tables, w.seq_lens)
+        if ev is not None:
+            ev[0].record()
+        out = paged_attention_decode_batched(w.q, w.k_cache, w.v_cache, w.block_tables,
+                                             w.seq_lens, w.scale)
+        if ev is not None:
+            ev[1].record()
+        return out
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+              for _ in range(args.steps)]
+    t_start = torch.cuda.Event(enable_timing=True)
+    t_end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t_start.record()
+    for i in range(args.steps):
+        step(args.warmup + i, events[i])
+    t_end.record()
+    torch.cuda.synchronize()
+    total_ms = t_start.elapsed_time(t_end)
+    attn_ms = [a.elapsed_time(b) for a, b in events]
+    attn_mean = statistics.fmean(attn_ms)
+    attn_med = statistics.median(attn_ms)
+
+    alg_bytes = base.algorithmic_bytes(unique=True)
+    logical_bytes = base.algorithmic_bytes(unique=False)
+    achieved = alg_bytes / (attn_mean * 1e-3) / 1e9
+    traffic = read_traffic() if args.workload == "long_context" else None
+
+    result = {
+        "metric": "paged-decode attention HBM GB/s (% of peak) + decode tokens/sec, 1 MI355X",
+        "value": round(achieved, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(total_ms / args.steps, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16 storage, f32 accumulate",
+        "data": "synthetic N(0,1), random block tables, seeded",
+        "config": {
+            "workload": base.name,
+            "num_seqs": base.num_seqs,
+            "num_q_heads": base.q.shape[1],
+            "num_kv_heads": hkv,
+            "head_dim": d,
+            "block_size": base.k_cache.shape[1],
+            "total_tokens": sum(base.lens),
+            "max_len": max(base.lens),
+            "pool_copies_rotated": len(copies),
+            **base.meta,
+        },
+        "attention_ms_mean": round(attn_mean, 5),
+        "attention_ms_median": round(attn_med, 5),
+        "algorithmic_bytes": alg_bytes,
+        "logical_bytes": logical_bytes,
+        "pct_of_hbm_peak": round(100 * achieved / HBM_PEAK_GBS, 2),
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 2),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": traffic,
+        },
+        "decode_tokens_per_s": None,
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(base, args.cpu_seconds)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,141 @@
+/*
+ * C ABI of the MI355X (gfx950) paged-decode attention library.
+ *
+ * Every entry point takes plain device pointers, element strides and sizes, and
+ * a HIP stream passed as `void*` (a hipStream_t; NULL means the default stream).
+ * No function allocates device memory: split-K scratch is passed in by the
+ * caller through `workspace`, sized by the matching *_workspace_bytes() call.
+ * Every launch is asynchronous on the given stream; nothing synchronises the host.
+ *
+ * Tensor layouts (element strides, fp16 = IEEE binary16):
+ *   q        [num_seqs, num_q_heads, head_dim]            stride of head_dim must be 1
+ *   k_cache  [num_blocks, block_size, num_kv_heads, head_dim]  (same for v_cache)
+ *   block_tables [num_seqs, max_blocks_per_seq] int32, seq_lens [num_seqs] int32
+ *   out      [num_seqs, num_q_heads, head_dim]
+ * Query head h reads KV head h / (num_q_heads / num_kv_heads).
+ *
+ * Return value: PA_OK (0) on success, otherwise a PA_ERR_* code; the message is
+ * available from pa_last_error() on the calling thread.
+ */
+#ifndef MI355X_PAGED_ATTENTION_H
+#define MI355X_PAGED_ATTENTION_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#if defined(__GNUC__)
+#define PA_API __attribute__((visibility("default")))
+#else
+#define PA_API
+#endif
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  PA_OK = 0,
+  PA_ERR_ARG = 1,          /* invalid argument: shapes, strides, alignment, null pointers */
+  PA_ERR_UNSUPPORTED = 2,  /* valid but not compiled: head_dim / group size outside the built set */
+  PA_ERR_WORKSPACE = 3,    /* workspace smaller than *_workspace_bytes() asked for */
+  PA_ERR_HIP = 4           /* the HIP runtime reported an error at launch */
+};
+
+/* ABI revision of this header; bumps whenever a signature changes. */
+PA_API int pa_abi_version(void);
+
+/* Message of the last failed call on this thread ("" after a success). */
+PA_API const char* pa_last_error(void);
+
+/*
+ * Batched GQA paged decode attention, online softmax with split-K partitions.
+ * Replaces paged_attention_decode_batched() and its Triton kernel,
+ * engine/kernels/paged_attention.py:508-698 (argument meaning :634-663).
+ * Tokens t < seq_lens[b] of sequence b are read from block
+ * block_tables[b][t / block_size], row t % block_size. seq_lens[b] <= 0 gives
+ * a zero output row; lengths beyond max_blocks_per_seq * block_size are clamped
+ * to it, and block ids outside [0, num_blocks) are clamped into range, so a bad
+ * table can give wrong numbers but never an out-of-bounds access.
+ * out must not alias q, the caches or the workspace.
+ */
+PA_API int pa_decode_batched_f16(const void* q, const int64_t q_strides[3],
+                          const void* k_cache, const int64_t k_strides[4],
+                          const void* v_cache, const int64_t v_strides[4],
+                          const int32_t* block_tables, const int64_t bt_strides[2],
+                          const int32_t* seq_lens,
+                          void* out, const int64_t out_strides[3],
+                          int num_seqs, int num_q_heads, int num_kv_heads, int head_dim,
+                          int block_size, int num_blocks, int max_blocks_per_seq,
+                          float scale, void* workspace, size_t workspace_bytes,
+                          void* stream);
+
+/* Workspace the call above needs for these sizes (0 is a valid answer). */
+PA_API size_t pa_decode_batched_workspace_bytes(int num_seqs, int num_q_heads, int num_kv_heads,
+                                         int head_dim, int block_size,
+                                         int max_blocks_per_seq);
+
+/*
+ * Single-sequence online-softmax decode attention.
+ * Replaces paged_attention_decode_v2(), engine/kernels/paged_attention.py:308-470.
+ * q/out are [num_q_heads, head_dim]; block_table is a 1-D int32 array of
+ * table_len entries with table_len >= ceil(seq_len / block_size)
+ * (the reference asserts the same, :443-446). seq_len is a host integer.
+ */
+PA_API int pa_decode_v2_f16(const void* q, const int64_t q_strides[2],
+                     const void* k_cache, const int64_t k_strides[4],
+                     const void* v_cache, const int64_t v_strides[4],
+                     const int32_t* block_table, int64_t bt_stride, int table_len,
+                     int seq_len, void* out, const int64_t out_strides[2],
+                     int num_q_heads, int num_kv_heads, int head_dim,
+                     int block_size, int num_blocks, float scale,
+                     void* workspace, size_t workspace_bytes, void* stream);
+
+PA_API size_t pa_decode_v2_workspace_bytes(int num_q_heads, int num_kv_heads, int head_dim,
+                                    int block_size, int table_len);
+
+/*
+ * Single-sequence two-pass decode attention: pass 1 the score maxima, a
+ * denominator pass, pass 2 the normalised probability-weighted V sum.
+ * Replaces paged_attention_decode_v1(), engine/kernels/paged_attention.py:102-305.
+ * K is read once: scores are kept in the workspace between the passes.
+ * Arguments as for pa_decode_v2_f16.
+ */
+PA_API int pa_decode_v1_f16(const void* q, const int64_t q_strides[2],
+                     const void* k_cache, const int64_t k_strides[4],
+                     const void* v_cache, const int64_t v_strides[4],
+                     const int32_t* block_table, int64_t bt_stride, int table_len,
+                     int seq_len, void* out, const int64_t out_strides[2],
+                     int num_q_heads, int num_kv_heads, int head_dim,
+                     int block_size, int num_blocks, float scale,
+                     void* workspace, size_t workspace_bytes, void* stream);
+
+PA_API size_t pa_decode_v1_workspace_bytes(int num_q_heads, int num_kv_heads, int head_dim,
+                                    int block_size, int seq_len);
+
+/*
+ * Per-step K/V write: for each sequence b with L = seq_lens[b] (or
+ * uniform_seq_len when seq_lens is NULL) and L >= 1, copies key[b, :, :] and
+ * value[b, :, :] bit for bit into k_cache/v_cache at block
+ * block_tables[b][(L-1) / block_size], row (L-1) % block_size, all kv heads.
+ * Replaces the per-sequence index_put loop of paged_decode_attention_forward,
+ * engine/kernels/paged_attention_integration.py:148-161 (single-sequence form
+ * :120-133), which has no function of its own in the reference.
+ * key/value are [num_seqs, num_kv_heads, head_dim] with any element strides.
+ * Rows whose slot falls outside the table or whose block id is outside
+ * [0, num_blocks) are skipped.
+ */
+PA_API int pa_kv_write_f16(const void* key, const int64_t key_strides[3],
+                    const void* value, const int64_t value_strides[3],
+                    void* k_cache, const int64_t k_strides[4],
+                    void* v_cache, const int64_t v_strides[4],
+                    const int32_t* block_tables, const int64_t bt_strides[2],
+                    const int32_t* seq_lens, int uniform_seq_len,
+                    int num_seqs, int num_kv_heads, int head_dim,
+                    int block_size, int num_blocks, int max_blocks_per_seq,
+                    void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MI355X_PAGED_ATTENTION_H */

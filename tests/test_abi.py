@@ -1,0 +1,100 @@
+"""The C-ABI library loads, exports every symbol the header declares, and validates
+arguments on the host before any GPU work (no GPU needed)."""
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+import torch  # noqa: F401  (loaded before the HIP library, as the bindings do)
+
+from engine.kernels import _native
+
+HEADER = Path(__file__).resolve().parent.parent / "include" / "paged_attention.h"
+
+
+def _declared_symbols():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"PA_API\s+[\w\s\*]+?\b(pa_\w+)\s*\(", text)))
+
+
+def test_header_declares_the_entry_points():
+    names = _declared_symbols()
+    for n in ["pa_decode_batched_f16", "pa_decode_v1_f16", "pa_decode_v2_f16", "pa_kv_write_f16",
+              "pa_last_error", "pa_abi_version"]:
+        assert n in names
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _native.load()
+    missing = [n for n in _declared_symbols() if not hasattr(lib, n)]
+    assert not missing, f"symbols declared in the header but not exported: {missing}"
+    assert set(_declared_symbols()) == set(_native.SIGNATURES), "bindings and header disagree"
+
+
+def test_abi_version():
+    assert _native.load().pa_abi_version() == _native.ABI_VERSION
+
+
+def test_workspace_sizes():
+    lib = _native.load()
+    # One split: no workspace.
+    assert lib.pa_decode_batched_workspace_bytes(8, 14, 2, 64, 16, 32) == 0
+    # 2048-block rows -> 32768 tokens -> 64 splits of 512 tokens.
+    rec = (32 + 16 * 64) * 4
+    assert lib.pa_decode_batched_workspace_bytes(256, 14, 2, 64, 16, 2048) == 256 * 2 * 64 * rec
+    assert lib.pa_decode_v1_workspace_bytes(14, 2, 64, 16, 67) == 2 * 16 * 80 * 4
+    assert lib.pa_decode_batched_workspace_bytes(8, 14, 2, 48, 16, 2048) == 0  # unsupported dim
+
+
+def _strides(*vals):
+    return _native.i64_array(vals)
+
+
+def _decode_call(lib, head_dim=64, nq=14, nkv=2, q=16, k=16, v=16, out=16, ws=0, max_blocks=4096,
+                 kstr=(2048, 128, 64, 1)):
+    return lib.pa_decode_batched_f16(
+        q, _strides(896, 64, 1), k, _strides(*kstr), v, _strides(*kstr),
+        16, _strides(max_blocks, 1), 16, out, _strides(896, 64, 1),
+        4, nq, nkv, head_dim, 16, 100, max_blocks, 0.125, ws, 0, None)
+
+
+def test_argument_errors_are_reported_before_launch():
+    lib = _native.load()
+    assert _decode_call(lib, head_dim=48) == _native.PA_ERR_UNSUPPORTED
+    assert b"head_dim 48" in lib.pa_last_error()
+    assert _decode_call(lib, nq=15, nkv=2) == _native.PA_ERR_ARG
+    assert b"divisible" in lib.pa_last_error()
+    assert _decode_call(lib, nq=34, nkv=2) == _native.PA_ERR_UNSUPPORTED
+    assert _decode_call(lib, q=0) == _native.PA_ERR_ARG
+    assert _decode_call(lib, k=8) == _native.PA_ERR_ARG  # misaligned pool pointer
+    assert _decode_call(lib, kstr=(2048, 128, 64, 2)) == _native.PA_ERR_ARG
+    assert _decode_call(lib) == _native.PA_ERR_WORKSPACE  # 4096-block rows need split-K scratch
+    assert b"workspace" in lib.pa_last_error()
+
+
+def test_kv_write_argument_errors():
+    lib = _native.load()
+    rc = lib.pa_kv_write_f16(0, _strides(128, 64, 1), 16, _strides(128, 64, 1), 16,
+                             _strides(2048, 128, 64, 1), 16, _strides(2048, 128, 64, 1), 16,
+                             _strides(4, 1), 16, 0, 4, 2, 64, 16, 100, 4, None)
+    assert rc == _native.PA_ERR_ARG
+    assert b"null" in lib.pa_last_error()
+
+
+def test_error_text_is_thread_local():
+    import threading
+
+    lib = _native.load()
+    assert _decode_call(lib, head_dim=48) == _native.PA_ERR_UNSUPPORTED
+    seen = {}
+
+    def other():
+        seen["msg"] = lib.pa_last_error()
+
+    t = threading.Thread(target=other)
+    t.start()
+    t.join()
+    assert seen["msg"] == b""
+    assert b"head_dim" in lib.pa_last_error()

@@ -1,0 +1,67 @@
+"""Host-side logic of the wrappers (no GPU): table padding and the reference's asserts."""
+from __future__ import annotations
+
+from types import SimpleNamespace
+
+import numpy as np
+import pytest
+import torch
+
+from engine.kernels.paged_attention import (
+    paged_attention_decode,
+    paged_attention_decode_batched,
+    paged_attention_decode_v1,
+    paged_attention_decode_v2,
+    pad_block_tables,
+)
+from engine.kernels.paged_attention_integration import PagedAttentionContext, paged_kv_write
+from oracle.paged_attention_oracle import pad_block_tables_reference
+
+
+def test_pad_block_tables_matches_spec():
+    tables = [[3, 1, 4], [], [1, 5], SimpleNamespace(physical_block_ids=[9, 2, 6, 5])]
+    got = pad_block_tables(tables, device="cpu")
+    assert got.dtype == torch.int32 and got.shape == (4, 4)
+    np.testing.assert_array_equal(got.numpy(), pad_block_tables_reference(tables))
+    np.testing.assert_array_equal(got.numpy(), [[3, 1, 4, 0], [0, 0, 0, 0], [1, 5, 0, 0], [9, 2, 6, 5]])
+
+
+def test_pad_block_tables_edge_cases():
+    assert pad_block_tables([], device="cpu").shape == (0, 0)
+    assert pad_block_tables([[], []], device="cpu").shape == (2, 1)  # at least one column
+    assert pad_block_tables([(7, 8)], device="cpu").tolist() == [[7, 8]]
+    with pytest.raises(TypeError):
+        pad_block_tables([{1, 2}], device="cpu")
+
+
+def _cpu_inputs():
+    q = torch.zeros(2, 14, 64, dtype=torch.float16)
+    k = torch.zeros(8, 16, 2, 64, dtype=torch.float16)
+    bt = torch.zeros(2, 4, dtype=torch.int32)
+    lens = torch.tensor([5, 9], dtype=torch.int32)
+    return q, k, bt, lens
+
+
+def test_wrappers_assert_like_the_reference():
+    q, k, bt, lens = _cpu_inputs()
+    with pytest.raises(AssertionError):
+        paged_attention_decode_batched(q, k, k, bt, lens, 0.125)  # CPU tensors
+    with pytest.raises(AssertionError):
+        paged_attention_decode_v1(q[0], k, k, bt[0], 5, 0.125)
+    with pytest.raises(AssertionError):
+        paged_attention_decode_v2(q[0], k, k, bt[0], 5, 0.125)
+    with pytest.raises(AssertionError):
+        paged_attention_decode(q, k, k, [[0], [1]], [5, 9], 0.125)
+    with pytest.raises(AssertionError):
+        paged_kv_write(q[:, :2], q[:, :2], k, k, bt, lens)
+
+
+def test_context_builds_padded_tables_and_lengths():
+    pool = SimpleNamespace(device=torch.device("cpu"), k_cache=[], v_cache=[])
+    ctx = PagedAttentionContext(pool, [[4, 2], SimpleNamespace(physical_block_ids=[7])], [20, 3])
+    assert ctx.is_batched
+    assert ctx.padded_block_tables.tolist() == [[4, 2], [7, 0]]
+    assert ctx.seq_lens_tensor.dtype == torch.int32 and ctx.seq_lens_tensor.tolist() == [20, 3]
+    single = PagedAttentionContext(pool, SimpleNamespace(physical_block_ids=[5, 6]), 17)
+    assert not single.is_batched and single.single_seq_len == 17
+    assert single.block_table_tensor.tolist() == [5, 6]

@@ -1,0 +1,388 @@
+// C ABI of the paged-attention library: argument checks, launch geometry and
+// error reporting. Declarations: include/paged_attention.h.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include <string>
+
+#include "../../include/paged_attention.h"
+#include "pa_common.h"
+
+namespace pa {
+
+static thread_local std::string g_error;
+
+void set_error(const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_error = buf;
+}
+
+void clear_error() { g_error.clear(); }
+
+// Tiles (16 tokens) per split-K partition for the batched entry point, and the
+// smaller split used for one sequence so that its kv heads still fill the GPU.
+constexpr int kSplitTilesBatched = 32;
+constexpr int kSplitTilesSingle = 8;
+
+static bool supported_head_dim(int D) { return D == 32 || D == 64 || D == 128 || D == 256; }
+
+static int split_tiles_for(int base, int bs) {
+  // Keep the block ids a split can touch within the LDS staging array.
+  const int64_t cap = ((int64_t)(kMaxIds - 2) * bs) / 16;
+  int64_t t = base < cap ? base : cap;
+  return t < 1 ? 1 : (int)t;
+}
+
+static int64_t max_tiles_for(int max_blocks, int bs) {
+  return ((int64_t)max_blocks * bs + 15) / 16;
+}
+
+static int64_t splits_for(int64_t tiles, int split_tiles) {
+  return tiles <= 0 ? 1 : (tiles + split_tiles - 1) / split_tiles;
+}
+
+static bool aligned(const void* p, size_t n) { return ((uintptr_t)p % n) == 0; }
+
+// Checks shared by every decode entry point. Mirrors the reference asserts
+// (engine/kernels/paged_attention.py:266-281, :648-662) plus what the kernels
+// need for 16-byte loads.
+static int check_common(const void* q, const void* k, const void* v, const void* out,
+                        const int64_t* k_strides, const int64_t* v_strides, int num_q_heads,
+                        int num_kv_heads, int head_dim, int block_size, int num_blocks) {
+  if (!q || !k || !v || !out || !k_strides || !v_strides) {
+    set_error("null pointer argument");
+    return PA_ERR_ARG;
+  }
+  if (num_q_heads <= 0 || num_kv_heads <= 0 || num_q_heads % num_kv_heads != 0) {
+    set_error("num_q_heads (%d) must be divisible by num_kv_heads (%d)", num_q_heads, num_kv_heads);
+    return PA_ERR_ARG;
+  }
+  if (num_q_heads / num_kv_heads > 16) {
+    set_error("query group size %d > 16 is not built", num_q_heads / num_kv_heads);
+    return PA_ERR_UNSUPPORTED;
+  }
+  if (!supported_head_dim(head_dim)) {
+    set_error("head_dim %d not built (32, 64, 128, 256)", head_dim);
+    return PA_ERR_UNSUPPORTED;
+  }
+  if (block_size <= 0 || num_blocks <= 0) {
+    set_error("block_size (%d) and num_blocks (%d) must be positive", block_size, num_blocks);
+    return PA_ERR_ARG;
+  }
+  for (int i = 0; i < 3; ++i) {
+    if (k_strides[i] % 8 || v_strides[i] % 8 || k_strides[i] < 0 || v_strides[i] < 0) {
+      set_error("cache strides must be non-negative multiples of 8 elements");
+      return PA_ERR_ARG;
+    }
+  }
+  if (k_strides[3] != 1 || v_strides[3] != 1) {
+    set_error("cache head_dim stride must be 1");
+    return PA_ERR_ARG;
+  }
+  if (!aligned(k, 16) || !aligned(v, 16) || !aligned(q, 16) || !aligned(out, 8)) {
+    set_error("q/k_cache/v_cache must be 16-byte aligned and out 8-byte aligned");
+    return PA_ERR_ARG;
+  }
+  return PA_OK;
+}
+
+static int finish_launch(hipError_t e) {
+  if (e != hipSuccess) {
+    set_error("HIP launch failed: %s", hipGetErrorString(e));
+    return PA_ERR_HIP;
+  }
+  return PA_OK;
+}
+
+}  // namespace pa
+
+using namespace pa;
+
+extern "C" {
+
+int pa_abi_version(void) { return 1; }
+
+const char* pa_last_error(void) { return g_error.c_str(); }
+
+size_t pa_decode_batched_workspace_bytes(int num_seqs, int num_q_heads, int num_kv_heads,
+                                         int head_dim, int block_size, int max_blocks_per_seq) {
+  (void)num_q_heads;
+  if (num_seqs <= 0 || num_kv_heads <= 0 || block_size <= 0 || max_blocks_per_seq <= 0 ||
+      !supported_head_dim(head_dim))
+    return 0;
+  const int st = split_tiles_for(kSplitTilesBatched, block_size);
+  const int64_t ms = splits_for(max_tiles_for(max_blocks_per_seq, block_size), st);
+  if (ms <= 1) return 0;
+  return (size_t)num_seqs * num_kv_heads * ms * record_floats(head_dim) * sizeof(float);
+}
+
+int pa_decode_batched_f16(const void* q, const int64_t q_strides[3], const void* k_cache,
+                          const int64_t k_strides[4], const void* v_cache,
+                          const int64_t v_strides[4], const int32_t* block_tables,
+                          const int64_t bt_strides[2], const int32_t* seq_lens, void* out,
+                          const int64_t out_strides[3], int num_seqs, int num_q_heads,
+                          int num_kv_heads, int head_dim, int block_size, int num_blocks,
+                          int max_blocks_per_seq, float scale, void* workspace,
+                          size_t workspace_bytes, void* stream) {
+  clear_error();
+  if (num_seqs < 0) {
+    set_error("num_seqs must be >= 0");
+    return PA_ERR_ARG;
+  }
+  if (num_seqs == 0) return PA_OK;
+  int rc = check_common(q, k_cache, v_cache, out, k_strides, v_strides, num_q_heads,
+                        num_kv_heads, head_dim, block_size, num_blocks);
+  if (rc) return rc;
+  if (!q_strides || !out_strides || !bt_strides || !block_tables || !seq_lens) {
+    set_error("null pointer argument");
+    return PA_ERR_ARG;
+  }
+  if (q_strides[2] != 1 || out_strides[2] != 1 || q_strides[0] % 8 || q_strides[1] % 8 ||
+      out_strides[0] % 4 || out_strides[1] % 4) {
+    set_error("q needs unit head_dim stride and 8-element aligned seq/head strides; "
+              "out unit head_dim stride and 4-element aligned strides");
+    return PA_ERR_ARG;
+  }
+  if (max_blocks_per_seq <= 0) {
+    set_error("block table needs at least one column");
+    return PA_ERR_ARG;
+  }
+  if (num_seqs > 65535) {
+    set_error("num_seqs %d exceeds the grid limit 65535", num_seqs);
+    return PA_ERR_UNSUPPORTED;
+  }
+  const int st = split_tiles_for(kSplitTilesBatched, block_size);
+  const int64_t ms = splits_for(max_tiles_for(max_blocks_per_seq, block_size), st);
+  const size_t need = pa_decode_batched_workspace_bytes(num_seqs, num_q_heads, num_kv_heads,
+                                                        head_dim, block_size, max_blocks_per_seq);
+  if (need && (!workspace || workspace_bytes < need)) {
+    set_error("workspace of %zu bytes needed, %zu given", need, workspace_bytes);
+    return PA_ERR_WORKSPACE;
+  }
+  DecodeArgs a{};
+  a.q = (const f16*)q;
+  a.q_sb = q_strides[0];
+  a.q_sh = q_strides[1];
+  a.k = (const f16*)k_cache;
+  a.k_sb = k_strides[0];
+  a.k_st = k_strides[1];
+  a.k_sh = k_strides[2];
+  a.v = (const f16*)v_cache;
+  a.v_sb = v_strides[0];
+  a.v_st = v_strides[1];
+  a.v_sh = v_strides[2];
+  a.bt = block_tables;
+  a.bt_sb = bt_strides[0];
+  a.bt_sk = bt_strides[1];
+  a.lens = seq_lens;
+  a.uniform_len = 0;
+  a.out = (f16*)out;
+  a.o_sb = out_strides[0];
+  a.o_sh = out_strides[1];
+  a.ws = (float*)workspace;
+  a.hkv = num_kv_heads;
+  a.g = num_q_heads / num_kv_heads;
+  a.bs = block_size;
+  a.num_blocks = num_blocks;
+  a.max_blocks = max_blocks_per_seq;
+  a.split_tiles = st;
+  a.max_splits = (int)ms;
+  a.scale_log2 = scale * kLog2e;
+  return finish_launch(launch_decode_split(a, head_dim, num_seqs, (hipStream_t)stream));
+}
+
+// Shared by the single-sequence entry points.
+static int fill_single(DecodeArgs& a, const void* q, const int64_t q_strides[2],
+                       const void* k_cache, const int64_t k_strides[4], const void* v_cache,
+                       const int64_t v_strides[4], const int32_t* block_table, int64_t bt_stride,
+                       int table_len, int seq_len, void* out, const int64_t out_strides[2],
+                       int num_q_heads, int num_kv_heads, int head_dim, int block_size,
+                       int num_blocks, float scale) {
+  int rc = check_common(q, k_cache, v_cache, out, k_strides, v_strides, num_q_heads,
+                        num_kv_heads, head_dim, block_size, num_blocks);
+  if (rc) return rc;
+  if (!q_strides || !out_strides || !block_table) {
+    set_error("null pointer argument");
+    return PA_ERR_ARG;
+  }
+  if (q_strides[1] != 1 || out_strides[1] != 1 || q_strides[0] % 8 || out_strides[0] % 4) {
+    set_error("q/out need unit head_dim stride and aligned head strides");
+    return PA_ERR_ARG;
+  }
+  if (seq_len < 0) {
+    set_error("seq_len must be >= 0");
+    return PA_ERR_ARG;
+  }
+  const int64_t need_blocks = ((int64_t)seq_len + block_size - 1) / block_size;
+  if (table_len < need_blocks || table_len <= 0) {
+    set_error("block_table size (%d) smaller than needed (%lld)", table_len,
+              (long long)need_blocks);
+    return PA_ERR_ARG;
+  }
+  a = DecodeArgs{};
+  a.q = (const f16*)q;
+  a.q_sb = 0;
+  a.q_sh = q_strides[0];
+  a.k = (const f16*)k_cache;
+  a.k_sb = k_strides[0];
+  a.k_st = k_strides[1];
+  a.k_sh = k_strides[2];
+  a.v = (const f16*)v_cache;
+  a.v_sb = v_strides[0];
+  a.v_st = v_strides[1];
+  a.v_sh = v_strides[2];
+  a.bt = block_table;
+  a.bt_sb = 0;
+  a.bt_sk = bt_stride;
+  a.lens = nullptr;
+  a.uniform_len = seq_len;
+  a.out = (f16*)out;
+  a.o_sb = 0;
+  a.o_sh = out_strides[0];
+  a.hkv = num_kv_heads;
+  a.g = num_q_heads / num_kv_heads;
+  a.bs = block_size;
+  a.num_blocks = num_blocks;
+  a.max_blocks = table_len;
+  a.scale_log2 = scale * kLog2e;
+  return PA_OK;
+}
+
+size_t pa_decode_v2_workspace_bytes(int num_q_heads, int num_kv_heads, int head_dim,
+                                    int block_size, int table_len) {
+  (void)num_q_heads;
+  if (num_kv_heads <= 0 || block_size <= 0 || table_len <= 0 || !supported_head_dim(head_dim))
+    return 0;
+  const int st = split_tiles_for(kSplitTilesSingle, block_size);
+  const int64_t ms = splits_for(max_tiles_for(table_len, block_size), st);
+  if (ms <= 1) return 0;
+  return (size_t)num_kv_heads * ms * record_floats(head_dim) * sizeof(float);
+}
+
+int pa_decode_v2_f16(const void* q, const int64_t q_strides[2], const void* k_cache,
+                     const int64_t k_strides[4], const void* v_cache, const int64_t v_strides[4],
+                     const int32_t* block_table, int64_t bt_stride, int table_len, int seq_len,
+                     void* out, const int64_t out_strides[2], int num_q_heads, int num_kv_heads,
+                     int head_dim, int block_size, int num_blocks, float scale, void* workspace,
+                     size_t workspace_bytes, void* stream) {
+  clear_error();
+  DecodeArgs a;
+  int rc = fill_single(a, q, q_strides, k_cache, k_strides, v_cache, v_strides, block_table,
+                       bt_stride, table_len, seq_len, out, out_strides, num_q_heads, num_kv_heads,
+                       head_dim, block_size, num_blocks, scale);
+  if (rc) return rc;
+  const int st = split_tiles_for(kSplitTilesSingle, block_size);
+  const int64_t ms = splits_for(max_tiles_for(table_len, block_size), st);
+  const size_t need =
+      pa_decode_v2_workspace_bytes(num_q_heads, num_kv_heads, head_dim, block_size, table_len);
+  if (need && (!workspace || workspace_bytes < need)) {
+    set_error("workspace of %zu bytes needed, %zu given", need, workspace_bytes);
+    return PA_ERR_WORKSPACE;
+  }
+  a.ws = (float*)workspace;
+  a.split_tiles = st;
+  a.max_splits = (int)ms;
+  return finish_launch(launch_decode_split(a, head_dim, 1, (hipStream_t)stream));
+}
+
+size_t pa_decode_v1_workspace_bytes(int num_q_heads, int num_kv_heads, int head_dim,
+                                    int block_size, int seq_len) {
+  (void)num_q_heads;
+  (void)head_dim;
+  (void)block_size;
+  if (num_kv_heads <= 0 || seq_len <= 0) return 0;
+  const int64_t lpad = ((int64_t)seq_len + 15) / 16 * 16;
+  return (size_t)num_kv_heads * 16 * lpad * sizeof(float);
+}
+
+int pa_decode_v1_f16(const void* q, const int64_t q_strides[2], const void* k_cache,
+                     const int64_t k_strides[4], const void* v_cache, const int64_t v_strides[4],
+                     const int32_t* block_table, int64_t bt_stride, int table_len, int seq_len,
+                     void* out, const int64_t out_strides[2], int num_q_heads, int num_kv_heads,
+                     int head_dim, int block_size, int num_blocks, float scale, void* workspace,
+                     size_t workspace_bytes, void* stream) {
+  clear_error();
+  DecodeArgs a;
+  int rc = fill_single(a, q, q_strides, k_cache, k_strides, v_cache, v_strides, block_table,
+                       bt_stride, table_len, seq_len, out, out_strides, num_q_heads, num_kv_heads,
+                       head_dim, block_size, num_blocks, scale);
+  if (rc) return rc;
+  const size_t need =
+      pa_decode_v1_workspace_bytes(num_q_heads, num_kv_heads, head_dim, block_size, seq_len);
+  if (need && (!workspace || workspace_bytes < need)) {
+    set_error("workspace of %zu bytes needed, %zu given", need, workspace_bytes);
+    return PA_ERR_WORKSPACE;
+  }
+  a.ws = (float*)workspace;
+  a.lpad = (int)(((int64_t)seq_len + 15) / 16 * 16);
+  return finish_launch(launch_decode_v1(a, head_dim, (hipStream_t)stream));
+}
+
+int pa_kv_write_f16(const void* key, const int64_t key_strides[3], const void* value,
+                    const int64_t value_strides[3], void* k_cache, const int64_t k_strides[4],
+                    void* v_cache, const int64_t v_strides[4], const int32_t* block_tables,
+                    const int64_t bt_strides[2], const int32_t* seq_lens, int uniform_seq_len,
+                    int num_seqs, int num_kv_heads, int head_dim, int block_size, int num_blocks,
+                    int max_blocks_per_seq, void* stream) {
+  clear_error();
+  if (num_seqs < 0) {
+    set_error("num_seqs must be >= 0");
+    return PA_ERR_ARG;
+  }
+  if (num_seqs == 0) return PA_OK;
+  if (!key || !value || !k_cache || !v_cache || !key_strides || !value_strides || !k_strides ||
+      !v_strides || !block_tables || !bt_strides) {
+    set_error("null pointer argument");
+    return PA_ERR_ARG;
+  }
+  if (num_kv_heads <= 0 || head_dim <= 0 || block_size <= 0 || num_blocks <= 0 ||
+      max_blocks_per_seq <= 0) {
+    set_error("num_kv_heads, head_dim, block_size, num_blocks and the table width must be "
+              "positive");
+    return PA_ERR_ARG;
+  }
+  if (k_strides[3] != 1 || v_strides[3] != 1) {
+    set_error("cache head_dim stride must be 1");
+    return PA_ERR_ARG;
+  }
+  KVWriteArgs a{};
+  a.key = (const uint16_t*)key;
+  a.ks_b = key_strides[0];
+  a.ks_h = key_strides[1];
+  a.ks_d = key_strides[2];
+  a.val = (const uint16_t*)value;
+  a.vs_b = value_strides[0];
+  a.vs_h = value_strides[1];
+  a.vs_d = value_strides[2];
+  a.kc = (uint16_t*)k_cache;
+  a.kc_sb = k_strides[0];
+  a.kc_st = k_strides[1];
+  a.kc_sh = k_strides[2];
+  a.vc = (uint16_t*)v_cache;
+  a.vc_sb = v_strides[0];
+  a.vc_st = v_strides[1];
+  a.vc_sh = v_strides[2];
+  a.bt = block_tables;
+  a.bt_sb = bt_strides[0];
+  a.bt_sk = bt_strides[1];
+  a.lens = seq_lens;
+  a.uniform_len = uniform_seq_len;
+  a.num_seqs = num_seqs;
+  a.hkv = num_kv_heads;
+  a.D = head_dim;
+  a.bs = block_size;
+  a.num_blocks = num_blocks;
+  a.max_blocks = max_blocks_per_seq;
+  bool vec = head_dim % 8 == 0 && a.ks_d == 1 && a.vs_d == 1 && a.ks_b % 8 == 0 &&
+             a.ks_h % 8 == 0 && a.vs_b % 8 == 0 && a.vs_h % 8 == 0 && a.kc_sb % 8 == 0 &&
+             a.kc_st % 8 == 0 && a.kc_sh % 8 == 0 && a.vc_sb % 8 == 0 && a.vc_st % 8 == 0 &&
+             a.vc_sh % 8 == 0 && aligned(key, 16) && aligned(value, 16) && aligned(k_cache, 16) &&
+             aligned(v_cache, 16);
+  return finish_launch(launch_kv_write(a, vec, (hipStream_t)stream));
+}
+
+}  // extern "C"

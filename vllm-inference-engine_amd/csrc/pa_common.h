@@ -1,0 +1,83 @@
+// Shared definitions for the gfx950 paged-attention kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace pa {
+
+typedef _Float16 f16;
+typedef f16 f16x4 __attribute__((ext_vector_type(4)));
+typedef f16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr float kNegInf = -__builtin_huge_valf();
+constexpr float kLog2e = 1.4426950408889634f;
+
+// Physical block ids of one split are staged in LDS; this bounds the split length.
+constexpr int kMaxIds = 512;
+
+// Host-side error reporting (thread-local message read by pa_last_error()).
+void set_error(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
+void clear_error();
+
+// Argument bundle of the decode kernels. Element strides; head_dim stride is 1.
+struct DecodeArgs {
+  const f16* q;
+  int64_t q_sb, q_sh;
+  const f16* k;
+  int64_t k_sb, k_st, k_sh;
+  const f16* v;
+  int64_t v_sb, v_st, v_sh;
+  const int32_t* bt;  // block table rows
+  int64_t bt_sb, bt_sk;
+  const int32_t* lens;  // per-sequence lengths, or null: use uniform_len
+  int uniform_len;
+  f16* out;
+  int64_t o_sb, o_sh;
+  float* ws;  // split-K partial records, or v1 score rows
+  int hkv, g, bs, num_blocks, max_blocks;
+  int split_tiles, max_splits;
+  int lpad;  // v1: padded score-row length
+  float scale_log2;  // softmax scale times log2(e): scores live in the exp2 domain
+};
+
+// Argument bundle of the K/V write kernel. Element strides; the sources may be
+// arbitrary views, the caches have unit head_dim stride.
+struct KVWriteArgs {
+  const uint16_t* key;
+  int64_t ks_b, ks_h, ks_d;
+  const uint16_t* val;
+  int64_t vs_b, vs_h, vs_d;
+  uint16_t* kc;
+  int64_t kc_sb, kc_st, kc_sh;
+  uint16_t* vc;
+  int64_t vc_sb, vc_st, vc_sh;
+  const int32_t* bt;
+  int64_t bt_sb, bt_sk;
+  const int32_t* lens;  // per-sequence lengths, or null: use uniform_len
+  int uniform_len;
+  int num_seqs, hkv, D, bs, num_blocks, max_blocks;
+};
+
+// Launchers (defined next to their kernels).
+hipError_t launch_decode_split(const DecodeArgs& a, int D, int num_seqs, hipStream_t s);
+hipError_t launch_decode_v1(const DecodeArgs& a, int D, hipStream_t s);
+hipError_t launch_kv_write(const KVWriteArgs& a, bool vec, hipStream_t s);
+
+// Length of sequence b clamped to [0, max_blocks * bs].
+__device__ inline int clamped_len(const DecodeArgs& a, int b) {
+  int L = a.lens ? a.lens[b] : a.uniform_len;
+  const int cap = a.max_blocks * a.bs;
+  return L < 0 ? 0 : (L > cap ? cap : L);
+}
+
+__device__ inline int num_splits_for(int ntiles, int split_tiles) {
+  return ntiles ? (ntiles + split_tiles - 1) / split_tiles : 1;
+}
+
+// Floats in one split-K partial record for head_dim D: 16 maxima (exp2 domain),
+// 16 denominators, then 16 x D unnormalised accumulators (row = q head in group).
+__host__ __device__ constexpr int record_floats(int D) { return 32 + 16 * D; }
+
+}  // namespace pa

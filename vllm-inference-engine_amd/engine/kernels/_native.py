@@ -1,0 +1,104 @@
+"""ctypes binding of libpa_gfx950.so, the gfx950 paged-attention library.
+
+The C ABI is declared in include/paged_attention.h. torch is imported before
+the library is opened: torch ships the HIP runtime as libamdhip64.so with the
+SONAME libamdhip64.so.7, and the library's own dependency on that SONAME then
+binds to the copy torch already loaded, so both share one runtime.
+
+There is no fallback: when the library is missing every entry point raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+
+import torch  # noqa: F401  (must be loaded before the HIP library, see above)
+
+LIB_NAME = "libpa_gfx950.so"
+LIB_PATH = Path(__file__).with_name(LIB_NAME)
+ABI_VERSION = 1
+
+PA_OK = 0
+PA_ERR_ARG = 1
+PA_ERR_UNSUPPORTED = 2
+PA_ERR_WORKSPACE = 3
+PA_ERR_HIP = 4
+
+_i32 = ctypes.c_int
+_i64 = ctypes.c_int64
+_f32 = ctypes.c_float
+_vp = ctypes.c_void_p
+_sz = ctypes.c_size_t
+_i64p = ctypes.POINTER(ctypes.c_int64)
+
+# name -> (restype, argtypes); every symbol include/paged_attention.h declares.
+SIGNATURES: dict[str, tuple] = {
+    "pa_abi_version": (_i32, []),
+    "pa_last_error": (ctypes.c_char_p, []),
+    "pa_decode_batched_f16": (_i32, [
+        _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _vp, _i64p,
+        _i32, _i32, _i32, _i32, _i32, _i32, _i32, _f32, _vp, _sz, _vp]),
+    "pa_decode_batched_workspace_bytes": (_sz, [_i32, _i32, _i32, _i32, _i32, _i32]),
+    "pa_decode_v2_f16": (_i32, [
+        _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64, _i32, _i32, _vp, _i64p,
+        _i32, _i32, _i32, _i32, _i32, _f32, _vp, _sz, _vp]),
+    "pa_decode_v2_workspace_bytes": (_sz, [_i32, _i32, _i32, _i32, _i32]),
+    "pa_decode_v1_f16": (_i32, [
+        _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64, _i32, _i32, _vp, _i64p,
+        _i32, _i32, _i32, _i32, _i32, _f32, _vp, _sz, _vp]),
+    "pa_decode_v1_workspace_bytes": (_sz, [_i32, _i32, _i32, _i32, _i32]),
+    "pa_kv_write_f16": (_i32, [
+        _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i32,
+        _i32, _i32, _i32, _i32, _i32, _i32, _vp]),
+}
+
+_lib = None
+_lock = threading.Lock()
+
+
+class NativeLibraryError(RuntimeError):
+    """The gfx950 library is missing, stale, or reported a failure."""
+
+
+def load() -> ctypes.CDLL:
+    """Open the library once and declare every exported signature."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not LIB_PATH.exists():
+                raise NativeLibraryError(
+                    f"{LIB_PATH} is not built; run `python vllm-inference-engine_amd/build.py` "
+                    "(there is no non-HIP fallback)")
+            lib = ctypes.CDLL(str(LIB_PATH))
+            for name, (res, args) in SIGNATURES.items():
+                fn = getattr(lib, name)
+                fn.restype = res
+                fn.argtypes = args
+            ver = lib.pa_abi_version()
+            if ver != ABI_VERSION:
+                raise NativeLibraryError(
+                    f"{LIB_PATH} has ABI {ver}, the bindings expect {ABI_VERSION}; rebuild it")
+            _lib = lib
+    return _lib
+
+
+def i64_array(values) -> ctypes.Array:
+    vals = [int(v) for v in values]
+    return (ctypes.c_int64 * len(vals))(*vals)
+
+
+def ptr(t: torch.Tensor) -> int:
+    return t.data_ptr()
+
+
+def stream_handle(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def check(status: int, what: str) -> None:
+    if status != PA_OK:
+        msg = load().pa_last_error().decode(errors="replace")
+        raise NativeLibraryError(f"{what} failed (status {status}): {msg}")

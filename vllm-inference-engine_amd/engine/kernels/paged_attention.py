@@ -1,0 +1,239 @@
+"""Paged decode attention on MI355X: the reference's Python operator API over HIP kernels.
+
+Same entry points, argument meaning, asserts and return values as the
+reference module engine/kernels/paged_attention.py; every compute call runs a
+hand-written gfx950 kernel from libpa_gfx950.so (C ABI in
+include/paged_attention.h). There is no CPU or Triton path: the kernels need
+CUDA(HIP) tensors, exactly as the reference's Triton entry points assert.
+
+Layouts (reference paged_attention.py:30-37, engine/memory/block_allocator.py:101):
+  q        [num_seqs, num_q_heads, head_dim] fp16
+  k_cache  [num_blocks, block_size, num_kv_heads, head_dim] fp16 (v_cache alike)
+  block_tables [num_seqs, max_blocks_per_seq] int32, seq_lens [num_seqs] int32
+Query head h reads kv head h // (num_q_heads // num_kv_heads).
+
+Differences from the reference, all on inputs the reference leaves undefined:
+  * seq_len 0 gives a zero output row (the Triton kernels divide 0 by 0);
+  * sequence lengths beyond the table width are clamped to it and block ids
+    outside the pool are clamped into it, so a malformed table cannot make the
+    kernel read outside the pool.
+"""
+from __future__ import annotations
+
+import math
+from typing import Any, Sequence
+
+import numpy as np
+import torch
+
+from . import _native
+
+__all__ = [
+    "paged_attention_decode",
+    "paged_attention_decode_v1",
+    "paged_attention_decode_v2",
+    "paged_attention_decode_batched",
+    "pad_block_tables",
+]
+
+
+def _q_ready(q: torch.Tensor) -> torch.Tensor:
+    """q with unit head_dim stride, 8-element aligned strides and a 16-byte aligned base."""
+    ok = (q.stride(-1) == 1 and all(s % 8 == 0 for s in q.stride()[:-1])
+          and q.data_ptr() % 16 == 0)
+    return q if ok else q.contiguous()
+
+
+def _workspace(nbytes: int, device: torch.device) -> torch.Tensor | None:
+    if nbytes == 0:
+        return None
+    return torch.empty(nbytes, dtype=torch.uint8, device=device)
+
+
+def paged_attention_decode_batched(
+    q: torch.Tensor,            # [num_seqs, num_q_heads, head_dim] (fp16, cuda)
+    k_cache: torch.Tensor,      # [num_blocks, block_size, num_kv_heads, head_dim] (fp16, cuda)
+    v_cache: torch.Tensor,      # [num_blocks, block_size, num_kv_heads, head_dim] (fp16, cuda)
+    block_tables: torch.Tensor, # [num_seqs, max_blocks_per_seq] (int32, cuda)
+    seq_lens: torch.Tensor,     # [num_seqs] (int32, cuda)
+    scale: float,
+) -> torch.Tensor:
+    """Batched GQA paged decode attention (reference paged_attention.py:634-698).
+
+    One launch covers every sequence; each (sequence, kv head) is cut into
+    split-K partitions processed by one wavefront each, with a log-sum-exp
+    merge when a sequence spans several partitions. Asynchronous on the
+    current stream, like the Triton launch it replaces.
+    """
+    assert q.is_cuda and k_cache.is_cuda and v_cache.is_cuda
+    assert block_tables.is_cuda and seq_lens.is_cuda
+    assert q.dtype == torch.float16 and k_cache.dtype == torch.float16 and v_cache.dtype == torch.float16
+    assert block_tables.dtype == torch.int32 and seq_lens.dtype == torch.int32
+
+    num_seqs, num_q_heads, head_dim = q.shape
+    num_blocks, block_size, num_kv_heads, head_dim_k = k_cache.shape
+    assert head_dim == head_dim_k, f"Head dimensions must match: {head_dim} vs {head_dim_k}"
+    assert num_q_heads % num_kv_heads == 0, (
+        f"num_q_heads ({num_q_heads}) must be divisible by num_kv_heads ({num_kv_heads})"
+    )
+    assert block_tables.shape[0] == num_seqs
+    assert seq_lens.shape[0] == num_seqs
+    assert v_cache.shape == k_cache.shape, "k_cache and v_cache must have the same shape"
+    assert block_tables.dim() == 2 and seq_lens.dim() == 1
+
+    q = _q_ready(q)
+    out = torch.empty_like(q)
+    if num_seqs == 0:
+        return out
+    max_blocks = block_tables.shape[1]
+    lib = _native.load()
+    ws_bytes = lib.pa_decode_batched_workspace_bytes(
+        num_seqs, num_q_heads, num_kv_heads, head_dim, block_size, max_blocks)
+    ws = _workspace(ws_bytes, q.device)
+    status = lib.pa_decode_batched_f16(
+        _native.ptr(q), _native.i64_array(q.stride()),
+        _native.ptr(k_cache), _native.i64_array(k_cache.stride()),
+        _native.ptr(v_cache), _native.i64_array(v_cache.stride()),
+        _native.ptr(block_tables), _native.i64_array(block_tables.stride()),
+        _native.ptr(seq_lens),
+        _native.ptr(out), _native.i64_array(out.stride()),
+        num_seqs, num_q_heads, num_kv_heads, head_dim, block_size, num_blocks, max_blocks,
+        float(scale), None if ws is None else ws.data_ptr(), ws_bytes,
+        _native.stream_handle(q.device))
+    _native.check(status, "pa_decode_batched_f16")
+    return out
+
+
+def _single_seq_args(q, k_cache, v_cache, block_table, seq_len):
+    assert q.is_cuda and k_cache.is_cuda and v_cache.is_cuda and block_table.is_cuda
+    assert q.dtype == torch.float16 and k_cache.dtype == torch.float16 and v_cache.dtype == torch.float16
+    assert block_table.dtype == torch.int32
+
+    num_q_heads, head_dim = q.shape
+    num_blocks, block_size, num_kv_heads, head_dim_k = k_cache.shape
+    assert head_dim == head_dim_k, f"Head dimensions must match: {head_dim} vs {head_dim_k}"
+    assert num_q_heads % num_kv_heads == 0, (
+        f"num_q_heads ({num_q_heads}) must be divisible by num_kv_heads ({num_kv_heads})"
+    )
+    num_blocks_for_seq = (seq_len + block_size - 1) // block_size
+    assert block_table.shape[0] >= num_blocks_for_seq, (
+        f"block_table size ({block_table.shape[0]}) smaller than needed ({num_blocks_for_seq})"
+    )
+    assert v_cache.shape == k_cache.shape, "k_cache and v_cache must have the same shape"
+    assert block_table.dim() == 1
+    return num_q_heads, head_dim, num_blocks, block_size, num_kv_heads
+
+
+def _single_seq_call(fn_name, ws_name, q, k_cache, v_cache, block_table, seq_len, scale, ws_last):
+    seq_len = int(seq_len)
+    num_q_heads, head_dim, num_blocks, block_size, num_kv_heads = _single_seq_args(
+        q, k_cache, v_cache, block_table, seq_len)
+    q = _q_ready(q)
+    out = torch.empty_like(q)
+    lib = _native.load()
+    table_len = block_table.shape[0]
+    if table_len == 0:
+        # Only reachable with seq_len == 0: nothing to attend to.
+        return out.zero_()
+    ws_bytes = getattr(lib, ws_name)(num_q_heads, num_kv_heads, head_dim, block_size,
+                                     ws_last(table_len, seq_len))
+    ws = _workspace(ws_bytes, q.device)
+    status = getattr(lib, fn_name)(
+        _native.ptr(q), _native.i64_array(q.stride()),
+        _native.ptr(k_cache), _native.i64_array(k_cache.stride()),
+        _native.ptr(v_cache), _native.i64_array(v_cache.stride()),
+        _native.ptr(block_table), int(block_table.stride(0)), table_len, seq_len,
+        _native.ptr(out), _native.i64_array(out.stride()),
+        num_q_heads, num_kv_heads, head_dim, block_size, num_blocks, float(scale),
+        None if ws is None else ws.data_ptr(), ws_bytes, _native.stream_handle(q.device))
+    _native.check(status, fn_name)
+    return out
+
+
+def paged_attention_decode_v1(
+    q: torch.Tensor,            # [num_q_heads, head_dim] (fp16, cuda)
+    k_cache: torch.Tensor,      # [num_blocks, block_size, num_kv_heads, head_dim] (fp16, cuda)
+    v_cache: torch.Tensor,      # [num_blocks, block_size, num_kv_heads, head_dim] (fp16, cuda)
+    block_table: torch.Tensor,  # 1D int32 cuda tensor of physical block IDs
+    seq_len: int,
+    scale: float,
+) -> torch.Tensor:
+    """Single-sequence two-pass decode attention (reference paged_attention.py:254-305).
+
+    Pass 1 computes every score and their maximum, a denominator pass sums the
+    exponentials, pass 2 accumulates the normalised probabilities times V.
+    Scores are kept in a workspace, so K is read once rather than three times.
+    """
+    return _single_seq_call("pa_decode_v1_f16", "pa_decode_v1_workspace_bytes",
+                            q, k_cache, v_cache, block_table, seq_len, scale,
+                            lambda table_len, n: n)
+
+
+def paged_attention_decode_v2(
+    q: torch.Tensor,            # [num_q_heads, head_dim] (fp16, cuda)
+    k_cache: torch.Tensor,      # [num_blocks, block_size, num_kv_heads, head_dim] (fp16, cuda)
+    v_cache: torch.Tensor,      # [num_blocks, block_size, num_kv_heads, head_dim] (fp16, cuda)
+    block_table: torch.Tensor,  # 1D int32 cuda tensor of physical block IDs
+    seq_len: int,
+    scale: float,
+) -> torch.Tensor:
+    """Single-sequence online-softmax decode attention (reference paged_attention.py:419-470)."""
+    return _single_seq_call("pa_decode_v2_f16", "pa_decode_v2_workspace_bytes",
+                            q, k_cache, v_cache, block_table, seq_len, scale,
+                            lambda table_len, n: table_len)
+
+
+def pad_block_tables(
+    block_tables: Sequence[Sequence[int]] | Sequence[Any],
+    device: torch.device | str = "cuda",
+) -> torch.Tensor:
+    """List of block-id lists (or objects with .physical_block_ids) -> int32 [num_seqs, max(1, max_len)].
+
+    Zero padded, like reference paged_attention.py:473-505; the padding is never
+    dereferenced because the kernels stop at each sequence's length. The table
+    is assembled on the host and copied to the device in one transfer.
+    """
+    num_seqs = len(block_tables)
+    if num_seqs == 0:
+        return torch.empty((0, 0), dtype=torch.int32, device=device)
+
+    raw_lists: list[list[int]] = []
+    for bt in block_tables:
+        if hasattr(bt, "physical_block_ids"):
+            raw_lists.append(list(bt.physical_block_ids))
+        elif isinstance(bt, (list, tuple)):
+            raw_lists.append(list(bt))
+        else:
+            raise TypeError(f"Unsupported block table type: {type(bt)}")
+
+    max_len = max((len(l) for l in raw_lists), default=0)
+    max_len = max(max_len, 1)
+    host = np.zeros((num_seqs, max_len), dtype=np.int32)
+    for i, row in enumerate(raw_lists):
+        if row:
+            host[i, :len(row)] = row
+    return torch.from_numpy(host).to(device)
+
+
+def paged_attention_decode(
+    q: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    block_tables: list[list[int]],
+    seq_lens: list[int],
+    scale: float,
+) -> torch.Tensor:
+    """List-based decode entry point (reference paged_attention.py:86-99).
+
+    The reference routes this name to its CPU oracle; here the lists are turned
+    into device tensors and the batched HIP kernel runs.
+    """
+    assert q.is_cuda, "paged_attention_decode runs on the GPU only"
+    tables = pad_block_tables(block_tables, device=q.device)
+    lens = torch.tensor([int(n) for n in seq_lens], dtype=torch.int32, device=q.device)
+    return paged_attention_decode_batched(q, k_cache, v_cache, tables, lens, scale)
+
+
+def default_scale(head_dim: int) -> float:
+    """1/sqrt(head_dim), the scale the reference integration falls back to (integration.py:114)."""
+    return 1.0 / math.sqrt(head_dim)
