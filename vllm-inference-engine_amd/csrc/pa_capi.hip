@@ -23,10 +23,9 @@ void set_error(const char* fmt, ...) {
 
 void clear_error() { g_error.clear(); }
 
-// Tiles (16 tokens) per split-K partition for the batched entry point, and the
-// smaller split used for one sequence so that its kv heads still fill the GPU.
+// Tiles (16 tokens) per split-K partition of the fixed-split path (batches larger
+// than the stream-K plan holds).
 constexpr int kSplitTilesBatched = 32;
-constexpr int kSplitTilesSingle = 8;
 
 static bool supported_head_dim(int D) { return D == 32 || D == 64 || D == 128 || D == 256; }
 
@@ -98,6 +97,54 @@ static int finish_launch(hipError_t e) {
   return PA_OK;
 }
 
+// ---- stream-K schedule: grid size and workspace layout ----
+
+// Upper bound of the workgroups a stream-K launch uses for these sizes (the
+// grid never exceeds the number of tiles).
+static int streamk_grid_bound(int num_seqs, int num_kv_heads, int head_dim, int block_size,
+                              int max_blocks) {
+  const int hg = streamk_head_group(num_kv_heads, head_dim);
+  const int64_t tiles = (int64_t)(num_kv_heads / hg) * num_seqs * max_tiles_for(max_blocks, block_size);
+  return (int)(tiles < kSkMaxWG ? (tiles < 1 ? 1 : tiles) : kSkMaxWG);
+}
+
+static size_t streamk_records_bytes(int num_kv_heads, int head_dim, int grid) {
+  const int hg = streamk_head_group(num_kv_heads, head_dim);
+  return (size_t)grid * 2 * hg * record_floats(head_dim) * sizeof(float);
+}
+
+static size_t streamk_workspace(int num_seqs, int num_kv_heads, int head_dim, int block_size,
+                                int max_blocks) {
+  const int grid = streamk_grid_bound(num_seqs, num_kv_heads, head_dim, block_size, max_blocks);
+  return streamk_records_bytes(num_kv_heads, head_dim, grid) + (size_t)(num_seqs + 1) * sizeof(int);
+}
+
+// Compute units of the current device (cached per device).
+static int device_cus() {
+  static int cache[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cache[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = 256;
+    cache[dev] = n;
+  }
+  return cache[dev];
+}
+
+// Fills the stream-K fields of `a` and launches; `ws` holds the records then the prefix.
+static hipError_t launch_streamk_with(DecodeArgs& a, int num_seqs, int head_dim, void* ws,
+                                      hipStream_t s) {
+  const int bound = streamk_grid_bound(num_seqs, a.hkv, head_dim, a.bs, a.max_blocks);
+  const int want = 2 * device_cus();
+  a.num_seqs = num_seqs;
+  a.num_wg = want < bound ? want : bound;
+  a.recs = (float*)ws;
+  a.pref = (int*)((char*)ws + streamk_records_bytes(a.hkv, head_dim, bound));
+  return launch_decode_streamk(a, head_dim, s);
+}
+
 }  // namespace pa
 
 using namespace pa;
@@ -114,6 +161,8 @@ size_t pa_decode_batched_workspace_bytes(int num_seqs, int num_q_heads, int num_
   if (num_seqs <= 0 || num_kv_heads <= 0 || block_size <= 0 || max_blocks_per_seq <= 0 ||
       !supported_head_dim(head_dim))
     return 0;
+  if (num_seqs <= kSkMaxSeqs)
+    return streamk_workspace(num_seqs, num_kv_heads, head_dim, block_size, max_blocks_per_seq);
   const int st = split_tiles_for(kSplitTilesBatched, block_size);
   const int64_t ms = splits_for(max_tiles_for(max_blocks_per_seq, block_size), st);
   if (ms <= 1) return 0;
@@ -192,6 +241,8 @@ int pa_decode_batched_f16(const void* q, const int64_t q_strides[3], const void*
   a.split_tiles = st;
   a.max_splits = (int)ms;
   a.scale_log2 = scale * kLog2e;
+  if (num_seqs <= kSkMaxSeqs)
+    return finish_launch(launch_streamk_with(a, num_seqs, head_dim, workspace, (hipStream_t)stream));
   return finish_launch(launch_decode_split(a, head_dim, num_seqs, (hipStream_t)stream));
 }
 
@@ -257,10 +308,7 @@ size_t pa_decode_v2_workspace_bytes(int num_q_heads, int num_kv_heads, int head_
   (void)num_q_heads;
   if (num_kv_heads <= 0 || block_size <= 0 || table_len <= 0 || !supported_head_dim(head_dim))
     return 0;
-  const int st = split_tiles_for(kSplitTilesSingle, block_size);
-  const int64_t ms = splits_for(max_tiles_for(table_len, block_size), st);
-  if (ms <= 1) return 0;
-  return (size_t)num_kv_heads * ms * record_floats(head_dim) * sizeof(float);
+  return streamk_workspace(1, num_kv_heads, head_dim, block_size, table_len);
 }
 
 int pa_decode_v2_f16(const void* q, const int64_t q_strides[2], const void* k_cache,
@@ -275,18 +323,13 @@ int pa_decode_v2_f16(const void* q, const int64_t q_strides[2], const void* k_ca
                        bt_stride, table_len, seq_len, out, out_strides, num_q_heads, num_kv_heads,
                        head_dim, block_size, num_blocks, scale);
   if (rc) return rc;
-  const int st = split_tiles_for(kSplitTilesSingle, block_size);
-  const int64_t ms = splits_for(max_tiles_for(table_len, block_size), st);
   const size_t need =
       pa_decode_v2_workspace_bytes(num_q_heads, num_kv_heads, head_dim, block_size, table_len);
   if (need && (!workspace || workspace_bytes < need)) {
     set_error("workspace of %zu bytes needed, %zu given", need, workspace_bytes);
     return PA_ERR_WORKSPACE;
   }
-  a.ws = (float*)workspace;
-  a.split_tiles = st;
-  a.max_splits = (int)ms;
-  return finish_launch(launch_decode_split(a, head_dim, 1, (hipStream_t)stream));
+  return finish_launch(launch_streamk_with(a, 1, head_dim, workspace, (hipStream_t)stream));
 }
 
 size_t pa_decode_v1_workspace_bytes(int num_q_heads, int num_kv_heads, int head_dim,

@@ -40,7 +40,17 @@ struct DecodeArgs {
   int split_tiles, max_splits;
   int lpad;  // v1: padded score-row length
   float scale_log2;  // softmax scale times log2(e): scores live in the exp2 domain
+  // Stream-K schedule (decode_streamk_kernel / merge_streamk_kernel).
+  int num_seqs;  // sequences in the batch
+  int num_wg;    // workgroups of the persistent grid
+  float* recs;   // 2 partial records per workgroup
+  int* pref;     // per-sequence exclusive tile prefix, num_seqs + 1 entries
 };
+
+// Stream-K limits: sequences whose tile prefix fits the LDS plan, and the
+// largest persistent grid the workspace is sized for.
+constexpr int kSkMaxSeqs = 1024;
+constexpr int kSkMaxWG = 1024;
 
 // Argument bundle of the K/V write kernel. Element strides; the sources may be
 // arbitrary views, the caches have unit head_dim stride.
@@ -64,6 +74,8 @@ struct KVWriteArgs {
 hipError_t launch_decode_split(const DecodeArgs& a, int D, int num_seqs, hipStream_t s);
 hipError_t launch_decode_v1(const DecodeArgs& a, int D, hipStream_t s);
 hipError_t launch_kv_write(const KVWriteArgs& a, bool vec, hipStream_t s);
+hipError_t launch_decode_streamk(const DecodeArgs& a, int D, hipStream_t s);
+int streamk_head_group(int num_kv_heads, int D);
 
 // Length of sequence b clamped to [0, max_blocks * bs].
 __device__ inline int clamped_len(const DecodeArgs& a, int b) {

@@ -90,12 +90,47 @@ def i64_array(values) -> ctypes.Array:
     return (ctypes.c_int64 * len(vals))(*vals)
 
 
+_arrays: dict[tuple, ctypes.Array] = {}
+
+
+def strides_of(t: torch.Tensor) -> ctypes.Array:
+    """The tensor's element strides as a ctypes int64 array (cached per stride tuple)."""
+    key = t.stride()
+    arr = _arrays.get(key)
+    if arr is None:
+        if len(_arrays) > 4096:
+            _arrays.clear()
+        arr = _arrays[key] = i64_array(key)
+    return arr
+
+
 def ptr(t: torch.Tensor) -> int:
     return t.data_ptr()
 
 
 def stream_handle(device: torch.device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
+
+
+_workspaces: dict[tuple, torch.Tensor] = {}
+
+
+def workspace(nbytes: int, device: torch.device, stream: int) -> int | None:
+    """Device address of a scratch buffer of at least nbytes for this (device, stream).
+
+    The buffer is kept and reused by later calls on the same stream; work on
+    one stream is ordered, so a call never overwrites scratch a previous call
+    on that stream still reads. Calls on different streams get different
+    buffers. Memory comes from torch's caching allocator.
+    """
+    if nbytes == 0:
+        return None
+    key = (device.index, stream)
+    buf = _workspaces.get(key)
+    if buf is None or buf.numel() < nbytes:
+        buf = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        _workspaces[key] = buf
+    return buf.data_ptr()
 
 
 def check(status: int, what: str) -> None:

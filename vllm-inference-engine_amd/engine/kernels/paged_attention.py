@@ -44,10 +44,25 @@ def _q_ready(q: torch.Tensor) -> torch.Tensor:
     return q if ok else q.contiguous()
 
 
-def _workspace(nbytes: int, device: torch.device) -> torch.Tensor | None:
-    if nbytes == 0:
+_ws_sizes: dict[tuple, int] = {}
+
+
+class _NoOp:
+    def __enter__(self):
         return None
-    return torch.empty(nbytes, dtype=torch.uint8, device=device)
+
+    def __exit__(self, *exc):
+        return False
+
+
+_NOOP = _NoOp()
+
+
+def _on_device(dev: torch.device):
+    """Make dev the current HIP device for the launch (a no-op when it already is)."""
+    if dev.index is None or dev.index == torch.cuda.current_device():
+        return _NOOP
+    return torch.cuda.device(dev)
 
 
 def paged_attention_decode_batched(
@@ -87,19 +102,22 @@ def paged_attention_decode_batched(
         return out
     max_blocks = block_tables.shape[1]
     lib = _native.load()
-    ws_bytes = lib.pa_decode_batched_workspace_bytes(
-        num_seqs, num_q_heads, num_kv_heads, head_dim, block_size, max_blocks)
-    ws = _workspace(ws_bytes, q.device)
-    status = lib.pa_decode_batched_f16(
-        _native.ptr(q), _native.i64_array(q.stride()),
-        _native.ptr(k_cache), _native.i64_array(k_cache.stride()),
-        _native.ptr(v_cache), _native.i64_array(v_cache.stride()),
-        _native.ptr(block_tables), _native.i64_array(block_tables.stride()),
-        _native.ptr(seq_lens),
-        _native.ptr(out), _native.i64_array(out.stride()),
-        num_seqs, num_q_heads, num_kv_heads, head_dim, block_size, num_blocks, max_blocks,
-        float(scale), None if ws is None else ws.data_ptr(), ws_bytes,
-        _native.stream_handle(q.device))
+    key = (num_seqs, num_q_heads, num_kv_heads, head_dim, block_size, max_blocks)
+    ws_bytes = _ws_sizes.get(key)
+    if ws_bytes is None:
+        ws_bytes = _ws_sizes[key] = lib.pa_decode_batched_workspace_bytes(*key)
+    dev = q.device
+    stream = _native.stream_handle(dev)
+    with _on_device(dev):
+        status = lib.pa_decode_batched_f16(
+            q.data_ptr(), _native.strides_of(q),
+            k_cache.data_ptr(), _native.strides_of(k_cache),
+            v_cache.data_ptr(), _native.strides_of(v_cache),
+            block_tables.data_ptr(), _native.strides_of(block_tables),
+            seq_lens.data_ptr(),
+            out.data_ptr(), _native.strides_of(out),
+            num_seqs, num_q_heads, num_kv_heads, head_dim, block_size, num_blocks, max_blocks,
+            float(scale), _native.workspace(ws_bytes, dev, stream), ws_bytes, stream)
     _native.check(status, "pa_decode_batched_f16")
     return out
 
@@ -137,15 +155,17 @@ def _single_seq_call(fn_name, ws_name, q, k_cache, v_cache, block_table, seq_len
         return out.zero_()
     ws_bytes = getattr(lib, ws_name)(num_q_heads, num_kv_heads, head_dim, block_size,
                                      ws_last(table_len, seq_len))
-    ws = _workspace(ws_bytes, q.device)
-    status = getattr(lib, fn_name)(
-        _native.ptr(q), _native.i64_array(q.stride()),
-        _native.ptr(k_cache), _native.i64_array(k_cache.stride()),
-        _native.ptr(v_cache), _native.i64_array(v_cache.stride()),
-        _native.ptr(block_table), int(block_table.stride(0)), table_len, seq_len,
-        _native.ptr(out), _native.i64_array(out.stride()),
-        num_q_heads, num_kv_heads, head_dim, block_size, num_blocks, float(scale),
-        None if ws is None else ws.data_ptr(), ws_bytes, _native.stream_handle(q.device))
+    dev = q.device
+    stream = _native.stream_handle(dev)
+    with _on_device(dev):
+        status = getattr(lib, fn_name)(
+            q.data_ptr(), _native.strides_of(q),
+            k_cache.data_ptr(), _native.strides_of(k_cache),
+            v_cache.data_ptr(), _native.strides_of(v_cache),
+            block_table.data_ptr(), int(block_table.stride(0)), table_len, seq_len,
+            out.data_ptr(), _native.strides_of(out),
+            num_q_heads, num_kv_heads, head_dim, block_size, num_blocks, float(scale),
+            _native.workspace(ws_bytes, dev, stream), ws_bytes, stream)
     _native.check(status, fn_name)
     return out
 

@@ -23,7 +23,7 @@ import torch
 import torch.nn as nn
 
 from . import _native
-from .paged_attention import pad_block_tables, paged_attention_decode_batched
+from .paged_attention import _on_device, pad_block_tables, paged_attention_decode_batched
 
 __all__ = [
     "PagedAttentionContext",
@@ -82,15 +82,17 @@ def paged_kv_write(
     if num_seqs == 0:
         return
     lib = _native.load()
-    status = lib.pa_kv_write_f16(
-        _native.ptr(key), _native.i64_array(key.stride()),
-        _native.ptr(value), _native.i64_array(value.stride()),
-        _native.ptr(k_cache), _native.i64_array(k_cache.stride()),
-        _native.ptr(v_cache), _native.i64_array(v_cache.stride()),
-        _native.ptr(block_tables), _native.i64_array(block_tables.stride()),
-        lens_ptr, uniform,
-        num_seqs, num_kv_heads, head_dim, block_size, num_blocks, block_tables.shape[1],
-        _native.stream_handle(key.device))
+    dev = key.device
+    with _on_device(dev):
+        status = lib.pa_kv_write_f16(
+            key.data_ptr(), _native.strides_of(key),
+            value.data_ptr(), _native.strides_of(value),
+            k_cache.data_ptr(), _native.strides_of(k_cache),
+            v_cache.data_ptr(), _native.strides_of(v_cache),
+            block_tables.data_ptr(), _native.strides_of(block_tables),
+            lens_ptr, uniform,
+            num_seqs, num_kv_heads, head_dim, block_size, num_blocks, block_tables.shape[1],
+            _native.stream_handle(dev))
     _native.check(status, "pa_kv_write_f16")
 
 
