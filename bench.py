@@ -41,11 +41,91 @@ def parse_args():
     p.add_argument("--workload", default="long_context",
                    help="long_context | gqa_sweep_kv{28,14,7,4} | qwen_layer | softmax_stress")
     p.add_argument("--copies", type=int, default=4, help="rotated pool copies (cache defeat)")
+    p.add_argument("--flush-mb", type=int, default=0,
+                   help="write this many MB before each step's attention call (cache defeat "
+                        "with one pool); outside the attention events, inside ms_per_step")
     p.add_argument("--seed", type=int, default=0)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=15.0,
                    help="approximate CPU time budget of the oracle baseline sample")
+    p.add_argument("--no-decode", action="store_true",
+                   help="skip the decode-step tokens/sec measurement")
+    p.add_argument("--decode-batch", type=int, default=128)
+    p.add_argument("--decode-steps", type=int, default=128)
     return p.parse_args()
+
+
+QWEN05 = dict(vocab_size=151936, hidden_size=896, intermediate_size=4864, num_hidden_layers=24,
+              num_attention_heads=14, num_key_value_heads=2, max_position_embeddings=32768,
+              rope_theta=1e6, rms_norm_eps=1e-6, tie_word_embeddings=False)
+
+
+def decode_benchmark(dev, seed, batch, steps):
+    """Greedy decode of a random-init Qwen2.5-0.5B-shaped model through the paged HIP path.
+
+    batch sequences with prompt lengths U[64, 1024] of random token ids; each
+    decode step runs the model with paged_kv_write + the batched paged-attention
+    kernel in all 24 layers. Prefill (transformers forward + prefill block copy)
+    is timed separately; tokens/sec counts decode steps only.
+    """
+    import numpy as np
+    import torch
+    from transformers import Qwen2Config, Qwen2ForCausalLM
+
+    from engine.kernels.paged_attention_integration import KernelPagedManualDecode
+    from engine.memory.block_pool import BlockTable
+    from types import SimpleNamespace
+
+    torch.manual_seed(seed)
+    with torch.device(dev):
+        model = Qwen2ForCausalLM(Qwen2Config(**QWEN05))
+    model = model.half().eval()
+    rng = np.random.default_rng(seed)
+    lens = rng.integers(64, 1025, size=batch)
+    prompts = [rng.integers(0, QWEN05["vocab_size"], size=int(n)).tolist() for n in lens]
+    bs = 16
+    need = sum((int(n) + steps + 2 * bs) // bs for n in lens)
+    runner = KernelPagedManualDecode(model, block_size=bs, num_blocks=need, device=str(dev))
+    alloc = runner.allocator
+    seqs = []
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i, p in enumerate(prompts):
+        bt = BlockTable(i, bs, [alloc.allocate() for _ in range((len(p) + bs - 1) // bs)], len(p))
+        seq = SimpleNamespace(seq_id=i, prompt_token_ids=p, block_table=bt, num_cached_tokens=0,
+                              last_token_id=None, last_logits=None, last_logit_margin=None)
+        seq.last_token_id = runner.prefill(seq)
+        seqs.append(seq)
+    torch.cuda.synchronize()
+    prefill_s = time.perf_counter() - t0
+
+    def one_step():
+        for q in seqs:
+            if q.block_table.num_tokens // bs >= len(q.block_table.physical_block_ids):
+                q.block_table.physical_block_ids.append(alloc.allocate())
+        for q, t in zip(seqs, runner.decode_step(seqs)):
+            q.last_token_id = t
+
+    warm = 2
+    for _ in range(warm):
+        one_step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps - warm):
+        one_step()
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    timed = steps - warm
+    return {
+        "tokens_per_s": round(batch * timed / dt, 1),
+        "ms_per_step": round(1e3 * dt / timed, 3),
+        "batch": batch,
+        "decode_steps_timed": timed,
+        "warmup_steps": warm,
+        "prefill_s": round(prefill_s, 3),
+        "model": "Qwen2.5-0.5B architecture, random init N(0, 0.02), fp16, untied lm_head",
+        "prompt_lens": "U[64, 1024], random token ids",
+    }
 
 
 def make_workload(name, device, seed):
@@ -136,8 +216,13 @@ def main():
     new_k = torch.randn(base.num_seqs, hkv, d, generator=g, device=dev).half()
     new_v = torch.randn(base.num_seqs, hkv, d, generator=g, device=dev).half()
 
+    flush = (torch.empty(args.flush_mb << 20, dtype=torch.uint8, device=dev)
+             if args.flush_mb > 0 else None)
+
     def step(i, ev=None):
         w = copies[i % len(copies)]
+        if flush is not None:
+            flush.fill_(i & 0xFF)
         paged_kv_write(new_k, new_v, w.k_cache, w.v_cache, w.block_tables, w.seq_lens)
         if ev is not None:
             ev[0].record()
@@ -193,6 +278,7 @@ def main():
             "total_tokens": sum(base.lens),
             "max_len": max(base.lens),
             "pool_copies_rotated": len(copies),
+            "flush_mb_per_step": args.flush_mb,
             **base.meta,
         },
         "attention_ms_mean": round(attn_mean, 5),
@@ -212,6 +298,12 @@ def main():
     }
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(base, args.cpu_seconds)
+    if not args.no_decode:
+        del copies, base
+        torch.cuda.empty_cache()
+        dec = decode_benchmark(dev, args.seed, args.decode_batch, args.decode_steps)
+        result["decode_tokens_per_s"] = dec["tokens_per_s"]
+        result["decode"] = dec
     print(json.dumps(result), flush=True)
 
 

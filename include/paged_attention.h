@@ -134,6 +134,23 @@ PA_API int pa_kv_write_f16(const void* key, const int64_t key_strides[3],
                     int block_size, int num_blocks, int max_blocks_per_seq,
                     void* stream);
 
+/*
+ * Prefill block copy: writes a prompt slice's K/V rows into whole cache blocks.
+ * Source block j (slice tokens j*block_size .. j*block_size + block_size - 1)
+ * goes to block block_ids[j]; rows at or past num_tokens are written as zeros.
+ * Replaces the per-layer pad + index_copy_ of _copy_prefill_kv,
+ * engine/kernels/paged_attention_integration.py:278-326. key/value are
+ * [num_tokens, num_kv_heads, head_dim] with any element strides (the
+ * permuted [Hkv, T, D] cache slice); block ids outside [0, num_blocks) are skipped.
+ */
+PA_API int pa_prefill_copy_f16(const void* key, const int64_t key_strides[3],
+                        const void* value, const int64_t value_strides[3],
+                        void* k_cache, const int64_t k_strides[4],
+                        void* v_cache, const int64_t v_strides[4],
+                        const int32_t* block_ids, int num_block_ids, int num_tokens,
+                        int num_kv_heads, int head_dim, int block_size, int num_blocks,
+                        void* stream);
+
 #ifdef __cplusplus
 }
 #endif

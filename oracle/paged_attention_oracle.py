@@ -12,6 +12,7 @@ file:line in the reference repository:
   pad_block_tables_reference       engine/kernels/paged_attention.py:473-505
   kv_write_reference               engine/kernels/paged_attention_integration.py:148-161
   kv_write_scatter                 same semantics, vectorised (cross-check of the loop)
+  prefill_copy_reference           engine/kernels/paged_attention_integration.py:278-326
 
 Pinning (tests/test_oracle.py): the attention oracle is checked against closed
 forms that do not share its code -- contiguous scaled-dot-product attention via
@@ -24,7 +25,10 @@ pool-slack invariance). tests/test_oracle_mutants.py plants plausible mistakes
 in copies of the oracle and shows each is caught. The K/V write is pinned
 bit-exactly by two independent statements (the reference's per-token loop and
 a vectorised scatter) and by block-id-encoded patterns. pad_block_tables is
-pinned by its specification (int32, zero padded, at least one column).
+pinned by its specification (int32, zero padded, at least one column). The
+prefill copy is pinned by the reference's own exact-content fixture
+(tests/test_paged_attention_prefix_cache.py:60-125, restated on the GPU in
+tests/test_gpu_prefill_copy.py) besides this restatement.
 """
 from __future__ import annotations
 
@@ -131,3 +135,24 @@ def kv_write_scatter(key: np.ndarray, value: np.ndarray, k_cache: np.ndarray, v_
     ids = block_tables[sel, pos // block_size]
     k_cache[ids, pos % block_size] = key[sel]
     v_cache[ids, pos % block_size] = value[sel]
+
+
+def prefill_copy_reference(k_src: torch.Tensor, v_src: torch.Tensor, k_cache: torch.Tensor,
+                           v_cache: torch.Tensor, block_ids: Sequence[int], num_tokens: int) -> None:
+    """Pad the token rows to whole blocks with zeros and index_copy_ them into the pool.
+
+    As engine/kernels/paged_attention_integration.py:308-326: k_src/v_src are
+    [tokens, num_kv_heads, head_dim] (tokens >= num_tokens, only the first
+    num_tokens used), cast to the pool dtype, padded (:315-317), viewed as
+    blocks (:319-320) and index_copy_'d at block_ids (:322-326).
+    """
+    bs = k_cache.shape[1]
+    nb = len(block_ids)
+    pad = nb * bs - num_tokens
+    ks, vs = k_src[:num_tokens], v_src[:num_tokens]
+    if pad > 0:
+        ks = torch.nn.functional.pad(ks, (0, 0, 0, 0, 0, pad))
+        vs = torch.nn.functional.pad(vs, (0, 0, 0, 0, 0, pad))
+    idx = torch.tensor(list(block_ids), dtype=torch.long)
+    k_cache.index_copy_(0, idx, ks.reshape(nb, bs, *ks.shape[1:]).to(k_cache.dtype))
+    v_cache.index_copy_(0, idx, vs.reshape(nb, bs, *vs.shape[1:]).to(v_cache.dtype))

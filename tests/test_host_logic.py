@@ -65,3 +65,49 @@ def test_context_builds_padded_tables_and_lengths():
     single = PagedAttentionContext(pool, SimpleNamespace(physical_block_ids=[5, 6]), 17)
     assert not single.is_batched and single.single_seq_len == 17
     assert single.block_table_tensor.tolist() == [5, 6]
+
+
+def _cpu_runner():
+    from engine.kernels.paged_attention_integration import KernelPagedManualDecode
+
+    model = SimpleNamespace(config=SimpleNamespace(num_hidden_layers=1, num_key_value_heads=2,
+                                                   head_dim=64, hidden_size=128,
+                                                   num_attention_heads=2))
+    return KernelPagedManualDecode(model, block_size=16, num_blocks=4, device="cpu")
+
+
+def test_runner_refuses_writes_without_a_block_or_into_shared_blocks():
+    """Host-side guards of decode_step (reference integration.py:580-592) run before any kernel."""
+    from engine.memory.block_pool import BlockTable
+
+    runner = _cpu_runner()
+    full = BlockTable(0, 16, [runner.allocator.allocate()], 16)  # block full, no next block
+    with pytest.raises(AssertionError, match="no allocated block"):
+        with torch.inference_mode():
+            runner.decode_step([SimpleNamespace(seq_id=0, block_table=full, last_token_id=1)])
+    b = runner.allocator.allocate()
+    runner.allocator.fork(b)
+    shared = BlockTable(1, 16, [b], 3)
+    with pytest.raises(AssertionError, match="shared block"):
+        with torch.inference_mode():
+            runner.decode_step([SimpleNamespace(seq_id=1, block_table=shared, last_token_id=1)])
+    assert shared.num_tokens == 3  # nothing was bumped
+    with pytest.raises(ValueError):
+        runner.prefill(SimpleNamespace(prompt_token_ids=None, prompt=None, block_table=shared))
+
+
+def test_free_list_allocator_counts_references():
+    from engine.memory.block_pool import BlockTable, FreeListAllocator
+
+    a = FreeListAllocator(3)
+    ids = [a.allocate() for _ in range(3)]
+    assert not a.can_allocate(1)
+    with pytest.raises(MemoryError):
+        a.allocate()
+    a.fork(ids[0])
+    t = BlockTable(0, 16, list(ids), 40)
+    assert t.num_blocks_needed_for(40) == 3 and t.last_block_has_space()
+    t.free(a)
+    assert a.num_free == 2 and a.ref_counts == {ids[0]: 1}
+    with pytest.raises(ValueError):
+        a.free(ids[1])

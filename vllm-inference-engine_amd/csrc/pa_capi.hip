@@ -428,4 +428,64 @@ int pa_kv_write_f16(const void* key, const int64_t key_strides[3], const void* v
   return finish_launch(launch_kv_write(a, vec, (hipStream_t)stream));
 }
 
+int pa_prefill_copy_f16(const void* key, const int64_t key_strides[3], const void* value,
+                        const int64_t value_strides[3], void* k_cache, const int64_t k_strides[4],
+                        void* v_cache, const int64_t v_strides[4], const int32_t* block_ids,
+                        int num_block_ids, int num_tokens, int num_kv_heads, int head_dim,
+                        int block_size, int num_blocks, void* stream) {
+  clear_error();
+  if (num_block_ids < 0 || num_tokens < 0) {
+    set_error("num_block_ids and num_tokens must be >= 0");
+    return PA_ERR_ARG;
+  }
+  if (num_block_ids == 0) return PA_OK;
+  if ((int64_t)num_tokens > (int64_t)num_block_ids * block_size) {
+    set_error("num_tokens (%d) exceeds the %d blocks given", num_tokens, num_block_ids);
+    return PA_ERR_ARG;
+  }
+  if (!k_cache || !v_cache || !key_strides || !value_strides || !k_strides || !v_strides ||
+      !block_ids || (num_tokens > 0 && (!key || !value))) {
+    set_error("null pointer argument");
+    return PA_ERR_ARG;
+  }
+  if (num_kv_heads <= 0 || head_dim <= 0 || block_size <= 0 || num_blocks <= 0) {
+    set_error("num_kv_heads, head_dim, block_size and num_blocks must be positive");
+    return PA_ERR_ARG;
+  }
+  if (k_strides[3] != 1 || v_strides[3] != 1) {
+    set_error("cache head_dim stride must be 1");
+    return PA_ERR_ARG;
+  }
+  PrefillCopyArgs a{};
+  a.key = (const uint16_t*)key;
+  a.ks_t = key_strides[0];
+  a.ks_h = key_strides[1];
+  a.ks_d = key_strides[2];
+  a.val = (const uint16_t*)value;
+  a.vs_t = value_strides[0];
+  a.vs_h = value_strides[1];
+  a.vs_d = value_strides[2];
+  a.kc = (uint16_t*)k_cache;
+  a.kc_sb = k_strides[0];
+  a.kc_st = k_strides[1];
+  a.kc_sh = k_strides[2];
+  a.vc = (uint16_t*)v_cache;
+  a.vc_sb = v_strides[0];
+  a.vc_st = v_strides[1];
+  a.vc_sh = v_strides[2];
+  a.ids = block_ids;
+  a.num_ids = num_block_ids;
+  a.num_tokens = num_tokens;
+  a.hkv = num_kv_heads;
+  a.D = head_dim;
+  a.bs = block_size;
+  a.num_blocks = num_blocks;
+  const bool vec = head_dim % 8 == 0 && a.ks_d == 1 && a.vs_d == 1 && a.ks_t % 8 == 0 &&
+                   a.ks_h % 8 == 0 && a.vs_t % 8 == 0 && a.vs_h % 8 == 0 && a.kc_sb % 8 == 0 &&
+                   a.kc_st % 8 == 0 && a.kc_sh % 8 == 0 && a.vc_sb % 8 == 0 &&
+                   a.vc_st % 8 == 0 && a.vc_sh % 8 == 0 && aligned(key, 16) &&
+                   aligned(value, 16) && aligned(k_cache, 16) && aligned(v_cache, 16);
+  return finish_launch(launch_prefill_copy(a, vec, (hipStream_t)stream));
+}
+
 }  // extern "C"

@@ -70,10 +70,26 @@ struct KVWriteArgs {
   int num_seqs, hkv, D, bs, num_blocks, max_blocks;
 };
 
+// Argument bundle of the prefill block copy: source rows [num_tokens, Hkv, D]
+// with any element strides, written block by block into the caches.
+struct PrefillCopyArgs {
+  const uint16_t* key;
+  int64_t ks_t, ks_h, ks_d;
+  const uint16_t* val;
+  int64_t vs_t, vs_h, vs_d;
+  uint16_t* kc;
+  int64_t kc_sb, kc_st, kc_sh;
+  uint16_t* vc;
+  int64_t vc_sb, vc_st, vc_sh;
+  const int32_t* ids;  // destination block of each source block
+  int num_ids, num_tokens, hkv, D, bs, num_blocks;
+};
+
 // Launchers (defined next to their kernels).
 hipError_t launch_decode_split(const DecodeArgs& a, int D, int num_seqs, hipStream_t s);
 hipError_t launch_decode_v1(const DecodeArgs& a, int D, hipStream_t s);
 hipError_t launch_kv_write(const KVWriteArgs& a, bool vec, hipStream_t s);
+hipError_t launch_prefill_copy(const PrefillCopyArgs& a, bool vec, hipStream_t s);
 hipError_t launch_decode_streamk(const DecodeArgs& a, int D, hipStream_t s);
 int streamk_head_group(int num_kv_heads, int D);
 

@@ -27,6 +27,8 @@ namespace pa {
 
 namespace {
 
+constexpr int kXcds = 8;  // accelerator complex dies of an MI355X, each with its own L2
+
 __device__ inline f16x8 zero8() { return f16x8{0, 0, 0, 0, 0, 0, 0, 0}; }
 __device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
@@ -69,7 +71,12 @@ void decode_streamk_kernel(DecodeArgs a) {
   constexpr int NTHR = 64 * NW;
   constexpr int VST = NT * HG * 16 * LS;  // halves of V staging per wavefront
   constexpr int CMB = HG * 16 * (D + 2);  // floats of merge state per wavefront
-  constexpr int WAVE_BYTES = (VST * 2 > CMB * 4 ? VST * 2 : CMB * 4);
+  // The merge state gets its own LDS when both fit two workgroups per CU; then
+  // no barrier is needed after a merge (the next merge's entry barrier orders
+  // it), so the merge's global stores never stall the wavefronts.
+  constexpr bool SEPARATE = NW * (VST * 2 + CMB * 4) + 8 * kSkMaxSeqs + 64 <= 80 * 1024;
+  constexpr int WAVE_BYTES = SEPARATE ? VST * 2 + CMB * 4 : (VST * 2 > CMB * 4 ? VST * 2 : CMB * 4);
+  constexpr int CMB_OFF = SEPARATE ? VST * 2 : 0;  // byte offset of the merge state
   constexpr int PER = kSkMaxSeqs / NTHR;  // sequences planned per thread
   constexpr int REC = record_floats(D);
   static_assert(PER * NTHR == kSkMaxSeqs, "plan layout");
@@ -88,7 +95,14 @@ void decode_streamk_kernel(DecodeArgs a) {
   const int NHG = a.hkv / HG;
   const int bs = BS > 0 ? BS : a.bs;
   const int G = gridDim.x;
-  const int wg = blockIdx.x;
+  // Workgroup i is dispatched to XCD i % 8. Renumber so that each XCD owns a
+  // contiguous run of ranges: neighbouring sequences (which is where shared
+  // prefix blocks sit) then run on the same XCD and share its L2.
+  const int wg = [&] {
+    const int n8 = G / kXcds, rem = G % kXcds;
+    const int xcd = blockIdx.x % kXcds, k = blockIdx.x / kXcds;
+    return xcd * n8 + (xcd < rem ? xcd : rem) + k;
+  }();
 
   // ---- plan: clamped lengths and the exclusive prefix of tiles per sequence ----
   {
@@ -166,8 +180,29 @@ void decode_streamk_kernel(DecodeArgs a) {
   char* my_smem = smem + wave * WAVE_BYTES;
   f16* vst = reinterpret_cast<f16*>(my_smem);
 
-  int64_t x = x0;
-  while (x < x1) {
+  // Segment order: a range starts with at most one segment that continues a
+  // pair begun in an earlier range. It is processed last, so every workgroup
+  // starts on the first tiles of a pair: the leading blocks of all sequences
+  // -- where sequences share prefix blocks -- are read close together in time
+  // and repeated reads of a shared block find it in the L2 / MALL.
+  int64_t cont_end = x0;  // end of the leading continuation segment (x0 if none)
+  {
+    const int64_t base0 = (int64_t)NHG * s_pref[b];
+    const int nt0 = s_pref[b + 1] - s_pref[b];
+    const int64_t ps0 = base0 + (x0 - base0) / nt0 * nt0;
+    if (ps0 < x0) cont_end = ps0 + nt0 < x1 ? ps0 + nt0 : x1;
+  }
+  const int b_cont = b;
+  if (cont_end > x0 && cont_end < x1 && cont_end >= (int64_t)NHG * s_pref[b + 1]) {
+    ++b;
+    while (b < B - 1 && s_pref[b + 1] == s_pref[b]) ++b;
+  }
+
+  for (int pass = 0; pass < 2; ++pass) {
+  int64_t x = pass == 0 ? cont_end : x0;
+  const int64_t x_end = pass == 0 ? x1 : cont_end;
+  if (pass == 1) b = b_cont;
+  while (x < x_end) {
     const int nt_b = s_pref[b + 1] - s_pref[b];
     const int64_t base = (int64_t)NHG * s_pref[b];
     const int hg0 = (int)((x - base) / nt_b);
@@ -345,8 +380,8 @@ void decode_streamk_kernel(DecodeArgs a) {
     }
 
     // ---- merge the wavefronts' states through LDS ----
-    float* cm = reinterpret_cast<float*>(my_smem);
-    __syncthreads();  // every wavefront is done with its V staging
+    float* cm = reinterpret_cast<float*>(my_smem + CMB_OFF);
+    __syncthreads();  // V staging done (aliased case); the previous merge is read
 #pragma unroll
     for (int hg = 0; hg < HG; ++hg) {
       float l = l_run[hg];
@@ -371,11 +406,11 @@ void decode_streamk_kernel(DecodeArgs a) {
       float M = kNegInf;
 #pragma unroll
       for (int w = 0; w < NW; ++w)
-        M = fmaxf(M, reinterpret_cast<const float*>(smem + w * WAVE_BYTES)[hg * 16 + hd]);
+        M = fmaxf(M, reinterpret_cast<const float*>(smem + w * WAVE_BYTES + CMB_OFF)[hg * 16 + hd]);
       float num = 0.f, den = 0.f;
 #pragma unroll
       for (int w = 0; w < NW; ++w) {
-        const float* c = reinterpret_cast<const float*>(smem + w * WAVE_BYTES);
+        const float* c = reinterpret_cast<const float*>(smem + w * WAVE_BYTES + CMB_OFF);
         const float mw = c[hg * 16 + hd];
         const float sc = mw == kNegInf ? 0.f : fast_exp2(mw - M);
         den += sc * c[HG * 16 + hg * 16 + hd];
@@ -393,13 +428,14 @@ void decode_streamk_kernel(DecodeArgs a) {
         rec[32 + hd * D + d] = num;
       }
     }
-    __syncthreads();  // LDS is reused by the next segment
+    if constexpr (!SEPARATE) __syncthreads();  // the merge state aliases V staging
 
     x = pend;
-    if (x >= (int64_t)NHG * s_pref[b + 1]) {
+    if (x < x_end && x >= (int64_t)NHG * s_pref[b + 1]) {
       ++b;
       while (b < B - 1 && s_pref[b + 1] == s_pref[b]) ++b;
     }
+  }
   }
 }
 

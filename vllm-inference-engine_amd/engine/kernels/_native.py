@@ -51,6 +51,9 @@ SIGNATURES: dict[str, tuple] = {
     "pa_kv_write_f16": (_i32, [
         _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i32,
         _i32, _i32, _i32, _i32, _i32, _i32, _vp]),
+    "pa_prefill_copy_f16": (_i32, [
+        _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i32, _i32,
+        _i32, _i32, _i32, _i32, _vp]),
 }
 
 _lib = None

@@ -8,10 +8,15 @@ engine/kernels/paged_attention_integration.py:
   * patch_paged_attention (reference :179-208): binds that forward onto every
     attention module of a model for the duration of a decode step.
 
+  * KernelPagedManualDecode (reference :211-731): prefill into the pool,
+    batched decode steps, single-sequence greedy generation.
+
 The reference writes K/V with a Python loop of two index_put calls per sequence
 and a device-to-host `.item()` per sequence per layer (:148-161). Here the
 write is one HIP launch, paged_kv_write(), that computes every slot on the
-device from the block tables and lengths, so a decode step has no host syncs.
+device from the block tables and lengths, so a decode step's layers make no
+host syncs. Prompt K/V go into the pool with one paged_prefill_copy launch per
+layer (reference pad + index_copy_, :278-326).
 """
 from __future__ import annotations
 
@@ -28,8 +33,10 @@ from .paged_attention import _on_device, pad_block_tables, paged_attention_decod
 __all__ = [
     "PagedAttentionContext",
     "paged_kv_write",
+    "paged_prefill_copy",
     "paged_decode_attention_forward",
     "patch_paged_attention",
+    "KernelPagedManualDecode",
 ]
 
 
@@ -221,3 +228,282 @@ def patch_paged_attention(model: nn.Module, context: PagedAttentionContext):
                 delattr(module, "_orig_attention_forward")
             if hasattr(module, "_paged_attention_context"):
                 delattr(module, "_paged_attention_context")
+
+
+def paged_prefill_copy(
+    key: torch.Tensor,        # [num_tokens, num_kv_heads, head_dim], any strides (fp16 or castable)
+    value: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    block_ids: torch.Tensor,  # 1-D int32 device tensor: destination block of each source block
+    num_tokens: int,
+) -> None:
+    """Write a prompt slice's K/V into whole pool blocks, zero-padding the last block.
+
+    Same pool contents as the reference's pad + index_copy_
+    (integration.py:278-326): source block j goes to block_ids[j]; rows at or
+    past num_tokens become zeros. Sources of another dtype are cast to fp16
+    first, as the reference's `.to(self.dtype)` does.
+    """
+    assert k_cache.is_cuda and v_cache.is_cuda and block_ids.is_cuda
+    assert k_cache.dtype == torch.float16 and v_cache.dtype == torch.float16
+    assert block_ids.dtype == torch.int32 and block_ids.dim() == 1
+    assert k_cache.shape == v_cache.shape
+    num_blocks, block_size, num_kv_heads, head_dim = k_cache.shape
+    if key.dtype != torch.float16:
+        key = key.to(torch.float16)
+    if value.dtype != torch.float16:
+        value = value.to(torch.float16)
+    assert key.shape[1:] == (num_kv_heads, head_dim) and value.shape == key.shape
+    assert key.shape[0] >= num_tokens
+    lib = _native.load()
+    dev = k_cache.device
+    with _on_device(dev):
+        status = lib.pa_prefill_copy_f16(
+            key.data_ptr(), _native.strides_of(key), value.data_ptr(), _native.strides_of(value),
+            k_cache.data_ptr(), _native.strides_of(k_cache),
+            v_cache.data_ptr(), _native.strides_of(v_cache),
+            block_ids.data_ptr(), block_ids.shape[0], int(num_tokens),
+            num_kv_heads, head_dim, block_size, num_blocks, _native.stream_handle(dev))
+    _native.check(status, "pa_prefill_copy_f16")
+
+
+def _seq_field(seq, name, default=None):
+    if isinstance(seq, dict):
+        return seq.get(name, default)
+    return getattr(seq, name, default)
+
+
+def _set_seq_field(seq, name, value):
+    if isinstance(seq, dict):
+        seq[name] = value
+    elif hasattr(seq, name):
+        setattr(seq, name, value)
+
+
+class KernelPagedManualDecode:
+    """Paged decode runner over the HIP kernels (reference integration.py:211-731).
+
+    prefill(seq): Hugging Face forward over the prompt, then the owned K/V
+    blocks are written into the pool with paged_prefill_copy (prefix modes
+    "off", "share", "full" as in the reference). decode_step(seqs): one
+    batched forward with paged_decode_attention_forward patched into every
+    attention module, so each layer runs paged_kv_write + the batched paged
+    attention kernel. The step makes one device-to-host transfer (tokens and
+    top-1/top-2 margins together) instead of the reference's per-sequence
+    logits copies (:643-651); `last_logits` stays on the device.
+    """
+
+    def __init__(
+        self,
+        model: nn.Module,
+        tokenizer: Any = None,
+        block_size: int = 16,
+        num_blocks: Optional[int] = None,
+        gpu_memory_utilization: float = 0.65,
+        device: str = "cuda",
+        dtype: torch.dtype = torch.float16,
+        debug_prefix_cache: bool = False,
+        prefix_mode: str = "off",
+    ):
+        from ..memory.block_pool import FreeListAllocator, PhysicalBlockPool
+
+        if prefix_mode not in ("off", "share", "full"):
+            raise ValueError(f"Unsupported prefix_mode {prefix_mode!r}; expected 'off', 'share', or 'full'.")
+        self.model = model
+        self.tokenizer = tokenizer
+        self.block_size = block_size
+        self.device = torch.device(device)
+        self.dtype = dtype
+        self.debug_prefix_cache = debug_prefix_cache
+        self.prefix_mode = prefix_mode
+        config = model.config
+        self.num_layers = getattr(config, "num_hidden_layers", 24)
+        self.num_kv_heads = getattr(config, "num_key_value_heads", 2)
+        self.head_dim = getattr(config, "head_dim", None) or (
+            config.hidden_size // config.num_attention_heads)
+        if num_blocks is None:
+            free, _ = torch.cuda.mem_get_info(self.device)
+            per_block = (2 * self.num_layers * block_size * self.num_kv_heads * self.head_dim
+                         * torch.tensor([], dtype=dtype).element_size())
+            num_blocks = max(1, int(free * gpu_memory_utilization) // per_block)
+        self.num_blocks = num_blocks
+        self.pool = PhysicalBlockPool(num_blocks=num_blocks, block_size=block_size,
+                                      num_layers=self.num_layers, num_kv_heads=self.num_kv_heads,
+                                      head_dim=self.head_dim, dtype=dtype, device=self.device)
+        self.allocator = FreeListAllocator(num_blocks)
+        self._grad_probed = False
+
+    # -- prefill -----------------------------------------------------------------
+    def _copy_prefill_kv(self, pkv: Any, block_table: Any, prompt_len: int, skip_blocks: int = 0) -> None:
+        """Write the owned prompt blocks of every layer (reference :278-326)."""
+        start_token = skip_blocks * self.block_size
+        if start_token >= prompt_len:
+            return
+        total_blocks = (prompt_len + self.block_size - 1) // self.block_size
+        if total_blocks - skip_blocks <= 0:
+            return
+        ids = torch.tensor(block_table.physical_block_ids[skip_blocks:total_blocks],
+                           dtype=torch.int32, device=self.device)
+        for layer_idx in range(self.num_layers):
+            if hasattr(pkv, "layers"):
+                keys, values = pkv.layers[layer_idx].keys, pkv.layers[layer_idx].values
+            else:
+                keys, values = pkv[layer_idx][0], pkv[layer_idx][1]
+            k_src = keys[0, :, start_token:prompt_len, :].permute(1, 0, 2)
+            v_src = values[0, :, start_token:prompt_len, :].permute(1, 0, 2)
+            paged_prefill_copy(k_src, v_src, self.pool.k_cache[layer_idx],
+                               self.pool.v_cache[layer_idx], ids, prompt_len - start_token)
+
+    def _build_cached_prefix(self, block_table: Any, cached_tokens: int):
+        """DynamicCache holding the cached prefix blocks (reference :364-392)."""
+        from transformers.cache_utils import DynamicCache, DynamicLayer
+
+        cache = DynamicCache()
+        nb = cached_tokens // self.block_size
+        ids = torch.tensor(block_table.physical_block_ids[:nb], dtype=torch.long, device=self.device)
+        for layer_idx in range(self.num_layers):
+            key = self.pool.k_cache[layer_idx].index_select(0, ids).flatten(0, 1)
+            value = self.pool.v_cache[layer_idx].index_select(0, ids).flatten(0, 1)
+            layer = DynamicLayer()
+            layer.keys = key.permute(1, 0, 2).unsqueeze(0).contiguous()
+            layer.values = value.permute(1, 0, 2).unsqueeze(0).contiguous()
+            layer.is_initialized = True
+            cache.layers.append(layer)
+        return cache
+
+    @torch.inference_mode()
+    def prefill(self, seq: Any, allocator: Any = None) -> int:
+        """Single-sequence prefill; the scheduler has allocated the blocks (reference :394-516)."""
+        ids = _seq_field(seq, "prompt_token_ids")
+        if ids:
+            input_ids = torch.tensor([list(ids)], dtype=torch.long, device=self.device)
+        else:
+            prompt = _seq_field(seq, "prompt")
+            if not prompt or self.tokenizer is None:
+                raise ValueError(f"Unable to extract prompt or prompt_token_ids from sequence: {seq}")
+            input_ids = self.tokenizer(prompt, return_tensors="pt").input_ids.to(self.device)
+            _set_seq_field(seq, "prompt_token_ids", input_ids[0].tolist())
+        prompt_len = input_ids.shape[1]
+        block_table = _seq_field(seq, "block_table")
+        if block_table is None:
+            raise RuntimeError("prefill() requires seq.block_table to be pre-populated by the scheduler.")
+        cached = _seq_field(seq, "num_cached_tokens", 0) or 0
+        if cached < 0 or cached > prompt_len or cached % self.block_size:
+            raise ValueError(f"num_cached_tokens={cached} must be a full-block prefix within "
+                             f"prompt_len={prompt_len} (block_size={self.block_size}).")
+        if cached // self.block_size > len(block_table.physical_block_ids):
+            raise ValueError("num_cached_tokens exceeds the number of blocks in the sequence table.")
+        if self.prefix_mode == "full" and cached:
+            prefix = self._build_cached_prefix(block_table, cached)
+            out = self.model(
+                input_ids=input_ids[:, cached:],
+                attention_mask=torch.ones((1, prompt_len), dtype=torch.long, device=self.device),
+                position_ids=torch.arange(cached, prompt_len, device=self.device).unsqueeze(0),
+                past_key_values=prefix, use_cache=True, logits_to_keep=1)
+        else:
+            out = self.model(input_ids=input_ids, use_cache=True, logits_to_keep=1)
+        self._copy_prefill_kv(out.past_key_values, block_table, prompt_len,
+                              skip_blocks=cached // self.block_size)
+        logits = out.logits[:, -1, :]
+        top2 = torch.topk(logits[0], k=2).values.double()
+        # float64 holds every token id exactly; one transfer for id and margin.
+        tok_margin = torch.stack([torch.argmax(logits[0]).double(), top2[0] - top2[1]]).tolist()
+        _set_seq_field(seq, "last_logits", logits[0].detach())
+        _set_seq_field(seq, "last_logit_margin", float(tok_margin[1]))
+        return int(tok_margin[0])
+
+    # -- decode ------------------------------------------------------------------
+    @torch.inference_mode()
+    def decode_step(self, seqs: List[Any], allocator: Any = None) -> List[int]:
+        """One batched decode step for the running sequences (reference :518-653)."""
+        n = len(seqs)
+        if n == 0:
+            return []
+        allocator = allocator or self.allocator
+        if not self._grad_probed:
+            self._grad_probed = True
+            assert not torch.is_grad_enabled(), "decode_step must run under torch.inference_mode()"
+        seq_lens: List[int] = []
+        tables: List[Any] = []
+        last_tokens: List[int] = []
+        for seq in seqs:
+            bt = _seq_field(seq, "block_table")
+            if bt is None:
+                raise ValueError("Sequence must provide a block_table attribute or dict key.")
+            widx = bt.num_tokens // self.block_size
+            if widx >= len(bt.physical_block_ids):
+                raise AssertionError(f"Decode write for seq {_seq_field(seq, 'seq_id', '?')} has no "
+                                     f"allocated block at logical index {widx}.")
+            wid = bt.physical_block_ids[widx]
+            if allocator.ref_counts.get(wid, 0) > 1:
+                raise AssertionError(f"Decode write for seq {_seq_field(seq, 'seq_id', '?')} would "
+                                     f"modify shared block {wid} with ref_count "
+                                     f"{allocator.ref_counts[wid]}.")
+            bt.num_tokens += 1
+            seq_lens.append(bt.num_tokens)
+            tables.append(bt)
+            last = _seq_field(seq, "last_token_id")
+            if last is None:
+                gen = _seq_field(seq, "generated_ids")
+                if not gen:
+                    raise ValueError("Sequence must provide last_token_id or non-empty generated_ids.")
+                last = gen[-1]
+            last_tokens.append(int(last))
+        input_ids = torch.tensor(last_tokens, dtype=torch.long, device=self.device).unsqueeze(1)
+        position_ids = torch.tensor([[L - 1] for L in seq_lens], dtype=torch.long, device=self.device)
+        ctx = PagedAttentionContext(self.pool, tables, seq_lens, self.block_size, True)
+        with patch_paged_attention(self.model, ctx):
+            out = self.model(input_ids=input_ids, position_ids=position_ids, use_cache=False)
+        logits = out.logits[:, -1, :]
+        top2 = torch.topk(logits, k=2, dim=-1).values.double()
+        # float64 holds every token id exactly: tokens and margins in one transfer.
+        both = torch.stack([torch.argmax(logits, dim=-1).double(), top2[:, 0] - top2[:, 1]])
+        toks, margins = both.tolist()
+        for i, seq in enumerate(seqs):
+            _set_seq_field(seq, "last_logits", logits[i].detach())
+            _set_seq_field(seq, "last_logit_margin", float(margins[i]))
+        return [int(t) for t in toks]
+
+    @torch.inference_mode()
+    def generate(self, prompt: Any, max_new_tokens: int = 16, allocator: Any = None,
+                 block_table: Any = None, return_logits_history: bool = False):
+        """Single-sequence greedy generation through the paged decode path (reference :655-731).
+
+        `prompt` is a string (needs a tokenizer) or a list of token ids.
+        """
+        from ..memory.block_pool import BlockTable
+
+        alloc = allocator or self.allocator
+        if isinstance(prompt, str):
+            input_ids = self.tokenizer(prompt, return_tensors="pt").input_ids.to(self.device)
+        else:
+            input_ids = torch.tensor([list(prompt)], dtype=torch.long, device=self.device)
+        prompt_len = input_ids.shape[1]
+        if block_table is None:
+            block_table = BlockTable(seq_id=0, block_size=self.block_size)
+        while len(block_table.physical_block_ids) < (prompt_len + self.block_size - 1) // self.block_size:
+            block_table.physical_block_ids.append(alloc.allocate())
+        block_table.num_tokens = prompt_len
+        out = self.model(input_ids=input_ids, use_cache=True)
+        self._copy_prefill_kv(out.past_key_values, block_table, prompt_len)
+        next_token = torch.argmax(out.logits[:, -1, :], dim=-1, keepdim=True)
+        generated = [int(next_token.item())]
+        history = [out.logits[:, -1, :]]
+        seq_len = prompt_len
+        for _ in range(1, max_new_tokens):
+            seq_len += 1
+            if not block_table.last_block_has_space():
+                block_table.physical_block_ids.append(alloc.allocate())
+            block_table.num_tokens += 1
+            ctx = PagedAttentionContext(self.pool, [block_table], [seq_len], self.block_size, True)
+            pos = torch.tensor([[seq_len - 1]], dtype=torch.long, device=self.device)
+            with patch_paged_attention(self.model, ctx):
+                step = self.model(input_ids=next_token, position_ids=pos, use_cache=False)
+            logits = step.logits[:, -1, :]
+            history.append(logits)
+            next_token = torch.argmax(logits, dim=-1, keepdim=True)
+            generated.append(int(next_token.item()))
+        if return_logits_history:
+            return generated, history
+        return generated
