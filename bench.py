@@ -155,6 +155,26 @@ def read_traffic():
     return None
 
 
+def copy_ceiling(dev, nbytes=2 << 30, iters=10):
+    """Plain device copy bandwidth (read + write bytes), the box's practical bandwidth line."""
+    import torch
+
+    x = torch.empty(nbytes // 2, dtype=torch.float16, device=dev).normal_()
+    y = torch.empty_like(x)
+    y.copy_(x)
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(iters):
+        y.copy_(x)
+    b.record()
+    torch.cuda.synchronize()
+    t = a.elapsed_time(b) * 1e-3 / iters
+    del x, y
+    torch.cuda.empty_cache()
+    return round(2 * nbytes / t / 1e9, 1)
+
+
 def cpu_baseline(w, budget_s):
     """The oracle's literal fp16 path (the reference's CPU PyTorch algorithm) on a sample."""
     import torch
@@ -296,6 +316,7 @@ def main():
         },
         "decode_tokens_per_s": None,
     }
+    result["copy_ceiling_gbps"] = copy_ceiling(dev)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(base, args.cpu_seconds)
     if not args.no_decode:

@@ -11,6 +11,7 @@ from __future__ import annotations
 
 import random
 
+import numpy as np
 import pytest
 import torch
 
@@ -237,3 +238,22 @@ def test_shared_blocks_across_sequences(cuda_device):
     """Several sequences listing the same physical blocks (prefix sharing) read them correctly."""
     w = workloads.long_context(device=cuda_device, seed=1, num_seqs=16)
     _check_workload(w)
+
+
+@pytest.mark.parametrize("d", [64, 128])
+def test_large_batch_fixed_split_path(cuda_device, d):
+    """More than 1024 sequences take the fixed 512-token split-K kernel and its merge."""
+    rng = np.random.default_rng(d)
+    lens = rng.integers(1, 1500, size=1100).tolist()
+    lens[0], lens[1], lens[2] = 0, 512, 1537
+    w = workloads.make_random(len(lens), 14 if d == 64 else 8, 2, d, lens, 16, seed=d,
+                              device=cuda_device)
+    out = paged_attention_decode_batched(w.q, w.k_cache, w.v_cache, w.block_tables, w.seq_lens,
+                                         w.scale)
+    torch.cuda.synchronize()
+    assert torch.count_nonzero(out[0]) == 0
+    seqs = [1, 2, 3, 500, 1099] + [int(i) for i in np.argsort(lens)[-3:]]
+    q, k, v, tables, ls = workloads.gather_subset(w, seqs)
+    err = max_err(out[seqs], oracle32(q, k, v, tables, ls, w.scale))
+    print(f"[parity] fixed-split path D{d}: max abs err {err:.3e}", flush=True)
+    assert err <= TOL
