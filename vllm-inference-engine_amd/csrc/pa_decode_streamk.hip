@@ -21,7 +21,7 @@
 // S^T = K Q^T on MFMA for the whole query group of each head (K read back in
 // the MFMA operand layout), and O^T += V^T P^T on MFMA with V^T read back
 // transposed (see pa_decode.hip for the operand layouts). Block ids are
-// fetched two chunks ahead and K/V one chunk ahead of the computation.
+// fetched three chunks ahead and K/V two chunks ahead of the computation.
 #include "pa_common.h"
 
 namespace pa {
@@ -47,6 +47,21 @@ __device__ inline void wave_lds_fence() {
 // against ~5.9 TB/s with default-policy loads.
 __device__ inline f16x8 load_stream(const f16* p) {
   return __builtin_nontemporal_load(reinterpret_cast<const f16x8*>(p));
+}
+
+// Same load from a wavefront-uniform base plus a 32-bit per-lane byte offset,
+// which maps to the saddr + voffset form of global_load.
+__device__ inline f16x8 load_stream_at(const char* base, uint32_t lane_off) {
+  return __builtin_nontemporal_load(reinterpret_cast<const f16x8*>(base + lane_off));
+}
+
+// Transposing LDS read (ds_read_b64_tr_b16): within each group of 16 lanes,
+// lane 4 r + q supplies the address of halves [4 q, 4 q + 4) of row r of a
+// 4 x 16 block, and lane j receives column j of that block (rows 0..3).
+__device__ inline f16x4 lds_read_tr16(const f16* p) {
+  typedef __attribute__((__vector_size__(4 * sizeof(__fp16)))) __fp16 v4h;
+  auto* lp = (__attribute__((address_space(3))) v4h*)(const_cast<f16*>(p));
+  return __builtin_bit_cast(f16x4, __builtin_amdgcn_ds_read_tr16_b64_v4f16(lp));
 }
 
 template <int BS>
@@ -79,27 +94,28 @@ void decode_streamk_kernel(DecodeArgs a) {
   constexpr int NTHR = 64 * NW;
   constexpr int CPR = HG * D / 8;          // 16-byte chunks per token row of a head group
   constexpr int NI = 16 * CPR / 64;        // load instructions per tile, for K and for V
-  constexpr int NID = (BS > 0 && BS % 16 == 0) ? 1 : NI;  // block ids per tile per lane
+  // A 16-token tile lies inside one block when 16 divides the block size: its
+  // block id and row base are then wavefront-uniform.
+  constexpr bool UNIFORM_TILE = BS > 0 && BS % 16 == 0;
+  constexpr int NID = UNIFORM_TILE ? 1 : NI;  // block ids per tile per lane
+  constexpr int RS = 64 / CPR;                // token rows one load instruction covers
   static_assert(NI * 64 == 16 * CPR, "tile must split into whole 64-lane loads");
-  constexpr int VST = NT * HG * 16 * LS;  // halves of V staging per wavefront
-  constexpr int CMB = HG * 16 * (D + 2);  // floats of merge state per wavefront
-  // The merge state gets its own LDS when both fit two workgroups per CU; then
-  // no barrier is needed after a merge (the next merge's entry barrier orders
-  // it), so the merge's global stores never stall the wavefronts.
-  constexpr bool SEPARATE = NW * (VST * 2 + CMB * 4) + 8 * kSkMaxSeqs + 64 <= 80 * 1024;
-  constexpr int WAVE_BYTES = SEPARATE ? VST * 2 + CMB * 4 : (VST * 2 > CMB * 4 ? VST * 2 : CMB * 4);
-  constexpr int CMB_OFF = SEPARATE ? VST * 2 : 0;  // byte offset of the merge state
+  static_assert(RS * CPR == 64, "a load instruction must cover whole rows");
+  constexpr int VST = NT * HG * 16 * LS;  // halves of one staging buffer (K or V) per wavefront
+  constexpr int CMB = 32 * HG + HG * ND * 64 * 4;  // floats of merge state per wavefront
+  // Per wavefront: a K and a V staging buffer; the merge state reuses the same
+  // bytes at segment ends.
+  constexpr int WAVE_BYTES = (2 * VST * 2 > CMB * 4 ? 2 * VST * 2 : CMB * 4);
   constexpr int PER = kSkMaxSeqs / NTHR;  // sequences planned per thread
   constexpr int REC = record_floats(D);
   static_assert(PER * NTHR == kSkMaxSeqs, "plan layout");
 
   __shared__ __attribute__((aligned(16))) char smem[NW * WAVE_BYTES];
   __shared__ int s_pref[kSkMaxSeqs + 1];
-  __shared__ int s_len[kSkMaxSeqs];
   __shared__ int s_wtot[NW];
 
   const int tid = threadIdx.x;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
   const int row = lane & 15;
   const int grp = lane >> 4;
@@ -124,11 +140,7 @@ void decode_streamk_kernel(DecodeArgs a) {
     for (int i = 0; i < PER; ++i) {
       const int b = tid * PER + i;
       int n = 0;
-      if (b < B) {
-        const int L = clamped_len(a, b);
-        s_len[b] = L;
-        n = (L + 15) >> 4;
-      }
+      if (b < B) n = (clamped_len(a, b) + 15) >> 4;
       cnt[i] = n;
       local += n;
     }
@@ -189,8 +201,18 @@ void decode_streamk_kernel(DecodeArgs a) {
     b = lo;
   }
 
+  // Byte offset of this lane's 16-byte piece within a tile, relative to the
+  // tile's first row at the group's first kv head (same for every tile).
+  uint32_t k_lane = 0, v_lane = 0;
+  if constexpr (UNIFORM_TILE) {
+    const int lrow = lane / CPR, lcol = (lane % CPR) * 8;
+    const int lhg = lcol / D, ld0 = lcol - lhg * D;
+    k_lane = (uint32_t)(2 * (lrow * a.k_st + lhg * a.k_sh + ld0));
+    v_lane = (uint32_t)(2 * (lrow * a.v_st + lhg * a.v_sh + ld0));
+  }
   char* my_smem = smem + wave * WAVE_BYTES;
-  f16* vst = reinterpret_cast<f16*>(my_smem);
+  f16* kst = reinterpret_cast<f16*>(my_smem);  // K staging
+  f16* vst = kst + VST;                          // V staging
 
   // Segment order: a range starts with at most one segment that continues a
   // pair begun in an earlier range. It is processed last, so every workgroup
@@ -224,7 +246,7 @@ void decode_streamk_kernel(DecodeArgs a) {
     const int s1 = (int)((x1 < pend ? x1 : pend) - pstart);
     const bool first = s0 == 0;
     const bool last = pend <= x1;
-    const int L = s_len[b];
+    const int L = clamped_len(a, b);
     const int h0 = hg0 * HG;  // first kv head of the group
 
     // ---- this wavefront's share of the segment ----
@@ -267,7 +289,19 @@ void decode_streamk_kernel(DecodeArgs a) {
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) {
         const int ti = s0 + k * NT + nt;
-        if (ti < s1) {
+        if constexpr (UNIFORM_TILE) {
+          if (ti < s1) {
+            const int64_t id = min(max(ids[nt][0], 0), a.num_blocks - 1);
+            const int64_t r0 = (ti * 16) % BS;
+            const char* kt = reinterpret_cast<const char*>(a.k + id * a.k_sb + r0 * a.k_st + (int64_t)h0 * a.k_sh);
+            const char* vt = reinterpret_cast<const char*>(a.v + id * a.v_sb + r0 * a.v_st + (int64_t)h0 * a.v_sh);
+#pragma unroll
+            for (int i = 0; i < NI; ++i) {
+              kb[nt][i] = load_stream_at(kt + 2 * (int64_t)(i * RS) * a.k_st, k_lane);
+              vb[nt][i] = load_stream_at(vt + 2 * (int64_t)(i * RS) * a.v_st, v_lane);
+            }
+          }
+        } else if (ti < s1) {
 #pragma unroll
           for (int i = 0; i < NI; ++i) {
             const int t = row_token(ti, nat_row(i));
@@ -284,20 +318,23 @@ void decode_streamk_kernel(DecodeArgs a) {
     };
     // Writes one tile's rows (natural layout) into the staging buffer laid out
     // [tile][head][row][LS]; rows past the sequence end are zeroed when asked.
-    auto stage = [&](int k, f16x8 (&buf)[NT][NI], bool zero_tail) {
+    auto stage = [&](int k, f16x8 (&buf)[NT][NI], f16* dst, bool zero_tail) {
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) {
         const int ti = s0 + k * NT + nt;
         if (ti < s1) {
+          if (zero_tail && ti * 16 + 16 > L) {  // wavefront-uniform: the last tile only
+#pragma unroll
+            for (int i = 0; i < NI; ++i)
+              if (ti * 16 + nat_row(i) >= L) buf[nt][i] = zero8();
+          }
 #pragma unroll
           for (int i = 0; i < NI; ++i) {
             const int r = nat_row(i);
             const int col = nat_col(i);
             const int hg = col / D;
             const int d0 = col - hg * D;
-            const bool valid = !zero_tail || ti * 16 + r < L;
-            *reinterpret_cast<f16x8*>(&vst[((nt * HG + hg) * 16 + r) * LS + d0]) =
-                valid ? buf[nt][i] : zero8();
+            *reinterpret_cast<f16x8*>(&dst[((nt * HG + hg) * 16 + r) * LS + d0]) = buf[nt][i];
           }
         }
       }
@@ -313,10 +350,14 @@ void decode_streamk_kernel(DecodeArgs a) {
       for (int i = 0; i < ND; ++i) acc[hg][i] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
 
-    auto compute = [&](int k, f16x8 (&kb)[NT][NI], f16x8 (&vb)[NT][NI]) {
-      // K through LDS into the MFMA operand layout (lane: token row, 8-wide k slice).
-      stage(k, kb, false);
+    // Both K and V of chunk k go to LDS first, which frees their registers for
+    // the loads of the chunk two steps ahead; the math then reads LDS only.
+    auto stage_both = [&](int k, f16x8 (&kb)[NT][NI], f16x8 (&vb)[NT][NI]) {
+      stage(k, kb, kst, false);
+      stage(k, vb, vst, true);  // V rows past the sequence end as zeros: 0 * garbage is never NaN
       wave_lds_fence();
+    };
+    auto compute = [&](int k) {
       float xs[NT][HG][4];
       float mloc[HG];
 #pragma unroll
@@ -327,26 +368,28 @@ void decode_streamk_kernel(DecodeArgs a) {
 #pragma unroll
         for (int hg = 0; hg < HG; ++hg) {
           if (ti < s1) {
-            const f16* kt = vst + ((nt * HG + hg) * 16 + row) * LS + grp * 8;
+            const f16* kt = kst + ((nt * HG + hg) * 16 + row) * LS + grp * 8;
             f32x4 s = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int c = 0; c < NC; ++c)
               s = __builtin_amdgcn_mfma_f32_16x16x32_f16(*reinterpret_cast<const f16x8*>(kt + 32 * c),
                                                          qf[hg][c], s, 0, 0, 0);
+            if (ti * 16 + 16 <= L) {  // wavefront-uniform: only the last tile is partial
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              const int tok = ti * 16 + grp * 4 + r;
-              const float xv = tok < L ? s[r] * a.scale_log2 : kNegInf;
-              xs[nt][hg][r] = xv;
-              mloc[hg] = fmaxf(mloc[hg], xv);
+              for (int r = 0; r < 4; ++r) xs[nt][hg][r] = s[r] * a.scale_log2;
+            } else {
+#pragma unroll
+              for (int r = 0; r < 4; ++r)
+                xs[nt][hg][r] = ti * 16 + grp * 4 + r < L ? s[r] * a.scale_log2 : kNegInf;
             }
+#pragma unroll
+            for (int r = 0; r < 4; ++r) mloc[hg] = fmaxf(mloc[hg], xs[nt][hg][r]);
           } else {
 #pragma unroll
             for (int r = 0; r < 4; ++r) xs[nt][hg][r] = kNegInf;
           }
         }
       }
-      wave_lds_fence();  // K reads are done before V takes the staging buffer
 #pragma unroll
       for (int hg = 0; hg < HG; ++hg) {
         float m = mloc[hg];
@@ -359,9 +402,6 @@ void decode_streamk_kernel(DecodeArgs a) {
         for (int i = 0; i < ND; ++i) acc[hg][i] *= alpha;
         m_run[hg] = m_new;
       }
-      // V rows to LDS (rows past the sequence end as zeros: 0 * garbage is never NaN).
-      stage(k, vb, true);
-      wave_lds_fence();
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) {
         const int ti = s0 + k * NT + nt;
@@ -377,12 +417,12 @@ void decode_streamk_kernel(DecodeArgs a) {
               ph[r] = hi;
               pl[r] = (f16)(pr - (float)hi);
             }
-            const f16* vt = vst + (nt * HG + hg) * 16 * LS;
+            // V^T operand: lane (row, grp) needs V[4 grp + r][16 nd + row], r = 0..3,
+            // which one transposing read of rows 4 grp..4 grp+3 delivers.
+            const f16* vt = vst + ((nt * HG + hg) * 16 + grp * 4 + (row >> 2)) * LS + (row & 3) * 4;
 #pragma unroll
             for (int nd = 0; nd < ND; ++nd) {
-              f16x4 av;
-#pragma unroll
-              for (int r = 0; r < 4; ++r) av[r] = vt[(grp * 4 + r) * LS + nd * 16 + row];
+              const f16x4 av = lds_read_tr16(vt + nd * 16);
               acc[hg][nd] = __builtin_amdgcn_mfma_f32_16x16x16f16(av, ph, acc[hg][nd], 0, 0, 0);
               acc[hg][nd] = __builtin_amdgcn_mfma_f32_16x16x16f16(av, pl, acc[hg][nd], 0, 0, 0);
             }
@@ -392,28 +432,41 @@ void decode_streamk_kernel(DecodeArgs a) {
       wave_lds_fence();
     };
 
+    // Wavefront-local pipeline over its chunks k = wave, wave + NW, ... (step
+    // s = 0, 1, ...): K/V register sets Y0/Y1 hold steps s and s+1, id sets
+    // X0/X1 hold the block ids two and three steps ahead. At step s: stage
+    // Y[s%2] into LDS, reuse it for the loads of step s+2 (ids in X[s%2]),
+    // fetch the ids of step s+3 into X[(s+1)%2], then compute step s.
     const int nck = (s1 - s0 + NT - 1) / NT;
-    int k = wave;
-    if (k < nck) {
+    if (wave < nck) {
       f16x8 kb0[NT][NI], vb0[NT][NI], kb1[NT][NI], vb1[NT][NI];
-      int idsA[NT][NID], idsB[NT][NID];
-      load_ids(k, idsA);
-      if (k + NW < nck) load_ids(k + NW, idsB);
-      load_kv(k, idsA, kb0, vb0);
-      for (; k < nck; k += 2 * NW) {
-        if (k + 2 * NW < nck) load_ids(k + 2 * NW, idsA);
-        if (k + NW < nck) load_kv(k + NW, idsB, kb1, vb1);
-        compute(k, kb0, vb0);
+      int ids0[NT][NID], ids1[NT][NID];
+      const int c0 = wave;
+      load_ids(c0, ids0);
+      if (c0 + NW < nck) load_ids(c0 + NW, ids1);
+      load_kv(c0, ids0, kb0, vb0);
+      if (c0 + NW < nck) load_kv(c0 + NW, ids1, kb1, vb1);
+      if (c0 + 2 * NW < nck) load_ids(c0 + 2 * NW, ids0);
+      for (int k = c0; k < nck; k += 2 * NW) {
+        stage_both(k, kb0, vb0);
+        if (k + 2 * NW < nck) load_kv(k + 2 * NW, ids0, kb0, vb0);
+        if (k + 3 * NW < nck) load_ids(k + 3 * NW, ids1);
+        compute(k);
         if (k + NW >= nck) break;
-        if (k + 3 * NW < nck) load_ids(k + 3 * NW, idsB);
-        if (k + 2 * NW < nck) load_kv(k + 2 * NW, idsA, kb0, vb0);
-        compute(k + NW, kb1, vb1);
+        stage_both(k + NW, kb1, vb1);
+        if (k + 3 * NW < nck) load_kv(k + 3 * NW, ids1, kb1, vb1);
+        if (k + 4 * NW < nck) load_ids(k + 4 * NW, ids0);
+        compute(k + NW);
       }
     }
 
     // ---- merge the wavefronts' states through LDS ----
-    float* cm = reinterpret_cast<float*>(my_smem + CMB_OFF);
-    __syncthreads();  // V staging done (aliased case); the previous merge is read
+    // Every wavefront stores its maxima and denominators per head and its
+    // accumulators in register layout (chunk j = hg * ND + nd: one f32x4 per
+    // lane, so the 16-byte LDS writes are conflict-free). Wavefront w then
+    // combines chunks j = w, w + NW, ... of all wavefronts and stores them.
+    float* cm = reinterpret_cast<float*>(my_smem);
+    __syncthreads();  // every wavefront is done with its staging buffers
 #pragma unroll
     for (int hg = 0; hg < HG; ++hg) {
       float l = l_run[hg];
@@ -425,42 +478,47 @@ void decode_streamk_kernel(DecodeArgs a) {
       }
 #pragma unroll
       for (int nd = 0; nd < ND; ++nd)
-        *reinterpret_cast<f32x4*>(&cm[2 * HG * 16 + (hg * 16 + row) * D + nd * 16 + grp * 4]) =
-            acc[hg][nd];
+        *reinterpret_cast<f32x4*>(&cm[32 * HG + ((hg * ND + nd) * 64 + lane) * 4]) = acc[hg][nd];
     }
     __syncthreads();
-    const int nout = HG * a.g * D;
-    for (int i = tid; i < nout; i += NTHR) {
-      const int hg = i / (a.g * D);
-      const int rem = i - hg * a.g * D;
-      const int hd = rem / D;
-      const int d = rem - hd * D;
+    for (int j = wave; j < HG * ND; j += NW) {
+      const int hg = j / ND;
+      const int nd = j - hg * ND;
+      float mw[NW];
       float M = kNegInf;
 #pragma unroll
-      for (int w = 0; w < NW; ++w)
-        M = fmaxf(M, reinterpret_cast<const float*>(smem + w * WAVE_BYTES + CMB_OFF)[hg * 16 + hd]);
-      float num = 0.f, den = 0.f;
+      for (int w = 0; w < NW; ++w) {
+        mw[w] = reinterpret_cast<const float*>(smem + w * WAVE_BYTES)[hg * 16 + row];
+        M = fmaxf(M, mw[w]);
+      }
+      float den = 0.f;
+      f32x4 num = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int w = 0; w < NW; ++w) {
-        const float* c = reinterpret_cast<const float*>(smem + w * WAVE_BYTES + CMB_OFF);
-        const float mw = c[hg * 16 + hd];
-        const float sc = mw == kNegInf ? 0.f : fast_exp2(mw - M);
-        den += sc * c[HG * 16 + hg * 16 + hd];
-        num += sc * c[2 * HG * 16 + (hg * 16 + hd) * D + d];
+        const float* c = reinterpret_cast<const float*>(smem + w * WAVE_BYTES);
+        const float sc = mw[w] == kNegInf ? 0.f : fast_exp2(mw[w] - M);
+        den += sc * c[HG * 16 + hg * 16 + row];
+        num += sc * *reinterpret_cast<const f32x4*>(&c[32 * HG + (j * 64 + lane) * 4]);
       }
-      if (first && last) {
-        a.out[(int64_t)b * a.o_sb + (int64_t)((h0 + hg) * a.g + hd) * a.o_sh + d] =
-            (f16)(den > 0.f ? num / den : 0.f);
-      } else {
-        float* rec = a.recs + ((int64_t)(wg * 2 + (first ? 1 : 0)) * HG + hg) * REC;
-        if (d == 0) {
-          rec[hd] = M;
-          rec[16 + hd] = den;
+      if (row < a.g) {
+        if (first && last) {
+          const float inv = den > 0.f ? 1.f / den : 0.f;
+          f16x4 o;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) o[r] = (f16)(num[r] * inv);
+          *reinterpret_cast<f16x4*>(a.out + (int64_t)b * a.o_sb +
+                                    (int64_t)((h0 + hg) * a.g + row) * a.o_sh + nd * 16 + grp * 4) = o;
+        } else {
+          float* rec = a.recs + ((int64_t)(wg * 2 + (first ? 1 : 0)) * HG + hg) * REC;
+          if (grp == 0 && nd == 0) {
+            rec[row] = M;
+            rec[16 + row] = den;
+          }
+          *reinterpret_cast<f32x4*>(&rec[32 + row * D + nd * 16 + grp * 4]) = num;
         }
-        rec[32 + hd * D + d] = num;
       }
     }
-    if constexpr (!SEPARATE) __syncthreads();  // the merge state aliases V staging
+    __syncthreads();  // the merge state aliases the staging buffers of the next segment
 
     x = pend;
     if (x < x_end && x >= (int64_t)NHG * s_pref[b + 1]) {
