@@ -137,9 +137,13 @@ static int device_cus() {
 static hipError_t launch_streamk_with(DecodeArgs& a, int num_seqs, int head_dim, void* ws,
                                       hipStream_t s) {
   const int bound = streamk_grid_bound(num_seqs, a.hkv, head_dim, a.bs, a.max_blocks);
-  const int want = 2 * device_cus();
+  const int want = kSkWgPerCu * device_cus();
   a.num_seqs = num_seqs;
   a.num_wg = want < bound ? want : bound;
+  // A pair segment costs a workgroup about as long as streaming 160 KB of K/V
+  // (measured on MI355X: pipeline fill plus the merge across wavefronts).
+  const int tile_bytes = 64 * streamk_head_group(a.hkv, head_dim) * head_dim;
+  a.seg_cost = (160 << 10) / tile_bytes;
   a.recs = (float*)ws;
   a.pref = (int*)((char*)ws + streamk_records_bytes(a.hkv, head_dim, bound));
   return launch_decode_streamk(a, head_dim, s);

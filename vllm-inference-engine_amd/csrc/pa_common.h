@@ -44,13 +44,18 @@ struct DecodeArgs {
   int num_seqs;  // sequences in the batch
   int num_wg;    // workgroups of the persistent grid
   float* recs;   // 2 partial records per workgroup
-  int* pref;     // per-sequence exclusive tile prefix, num_seqs + 1 entries
+  int* pref;     // per-sequence exclusive prefix of pair widths, num_seqs + 1 entries
+  // Fixed cost of a pair segment (pipeline fill, cross-wavefront merge),
+  // in tiles: the schedule splits tiles plus this cost per pair evenly.
+  int seg_cost;
 };
 
 // Stream-K limits: sequences whose tile prefix fits the LDS plan, and the
 // largest persistent grid the workspace is sized for.
 constexpr int kSkMaxSeqs = 1024;
 constexpr int kSkMaxWG = 1024;
+// Persistent workgroups per compute unit (each of eight wavefronts).
+constexpr int kSkWgPerCu = 1;
 
 // Argument bundle of the K/V write kernel. Element strides; the sources may be
 // arbitrary views, the caches have unit head_dim stride.

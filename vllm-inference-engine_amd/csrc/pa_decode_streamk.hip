@@ -2,16 +2,16 @@
 //
 // Schedule. The work is the list of (sequence, kv-head group) pairs, each a
 // run of 16-token tiles; the list is ordered sequence-major. A persistent grid
-// of G workgroups (two per CU, four wavefronts each) splits the concatenated
+// of G workgroups (one per CU, eight wavefronts each) splits the concatenated
 // tile list into G equal contiguous ranges, so every workgroup streams the
 // same number of bytes however skewed the sequence lengths are. Every
 // workgroup derives the plan itself: its threads load the lengths, scan the
 // per-sequence tile counts into LDS and binary-search their range's first pair.
 //
-// Within a range the workgroup walks pair segments. The four wavefronts take
-// the segment's chunks (NT tiles) round-robin, each keeping an online softmax
-// per query head, and merge their states through LDS at the end of the
-// segment. A pair wholly inside the range is written as final fp16 output; a
+// Within a range the workgroup walks pair segments. The eight wavefronts
+// claim the segment's chunks (NT tiles) from an LDS counter, each keeping an
+// online softmax per query head, and merge their states through LDS at the
+// end of the segment. A pair wholly inside the range is written as final fp16 output; a
 // pair cut by a range boundary leaves an fp32 partial record (at most two per
 // workgroup) that merge_streamk_kernel combines by log-sum-exp.
 //
@@ -31,6 +31,12 @@ namespace {
 constexpr int kXcds = 8;  // accelerator complex dies of an MI355X, each with its own L2
 
 __device__ inline f16x8 zero8() { return f16x8{0, 0, 0, 0, 0, 0, 0, 0}; }
+
+// K/V register buffers hold raw 16-byte pieces as 32-bit lanes: kept as fp16
+// vectors, the compiler merges a buffer array into one wide half vector and
+// splices new loads into it with half-word bit inserts, which must wait for
+// the loads at the splice instead of at the use.
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 __device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // Orders one wavefront's LDS writes before its later LDS reads (and reads
@@ -45,8 +51,8 @@ __device__ inline void wave_lds_fence() {
 // K/V rows are read with the non-temporal hint (global_load_dwordx4 ... nt):
 // measured on MI355X, random 4 KB block gathers reach ~6.6 TB/s with it
 // against ~5.9 TB/s with default-policy loads.
-__device__ inline f16x8 load_stream(const f16* p) {
-  return __builtin_nontemporal_load(reinterpret_cast<const f16x8*>(p));
+__device__ inline u32x4 load_stream(const f16* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
 }
 
 // Buffer resource over `bytes` bytes at a wavefront-uniform base. Loads at
@@ -62,8 +68,8 @@ __device__ inline __amdgpu_buffer_rsrc_t tile_rsrc(const void* base, int bytes) 
 // 16-byte K/V load through a tile resource: per-lane offset plus a uniform
 // offset, cache policy sc0 | nt (stream past the L1, non-temporal in L2) --
 // measured on MI355X at ~6.6 TB/s for random 4 KB block gathers.
-__device__ inline f16x8 load_tile(__amdgpu_buffer_rsrc_t r, uint32_t lane_off, int uoff) {
-  return __builtin_bit_cast(f16x8, __builtin_amdgcn_raw_buffer_load_b128(r, (int)lane_off, uoff, 3));
+__device__ inline u32x4 load_tile(__amdgpu_buffer_rsrc_t r, uint32_t lane_off, int uoff) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, (int)lane_off, uoff, 3);
 }
 
 // Transposing LDS read (ds_read_b64_tr_b16): within each group of 16 lanes,
@@ -132,6 +138,7 @@ void decode_streamk_kernel(DecodeArgs a) {
   __shared__ __attribute__((aligned(16))) char smem[NW * WAVE_BYTES];
   __shared__ int s_pref[kSkMaxSeqs + 1];
   __shared__ int s_wtot[NW];
+  __shared__ int s_next;  // next unclaimed chunk of the current segment
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -160,6 +167,7 @@ void decode_streamk_kernel(DecodeArgs a) {
       const int b = tid * PER + i;
       int n = 0;
       if (b < B) n = (clamped_len(a, b) + 15) >> 4;
+      if (n > 0) n += a.seg_cost;  // pair width: its tiles plus the segment overhead
       cnt[i] = n;
       local += n;
     }
@@ -184,7 +192,10 @@ void decode_streamk_kernel(DecodeArgs a) {
       if (b < B) s_pref[b] = run;
       run += cnt[i];
     }
-    if (tid == 0) s_pref[B] = total;
+    if (tid == 0) {
+      s_pref[B] = total;
+      s_next = 0;
+    }
     __syncthreads();
   }
   if (wg == 0 && a.pref) {
@@ -256,310 +267,335 @@ void decode_streamk_kernel(DecodeArgs a) {
   const int64_t x_end = pass == 0 ? x1 : cont_end;
   if (pass == 1) b = b_cont;
   while (x < x_end) {
-    const int nt_b = s_pref[b + 1] - s_pref[b];
+    const int nt_b = s_pref[b + 1] - s_pref[b];  // pair width, seg_cost included
     const int64_t base = (int64_t)NHG * s_pref[b];
     const int hg0 = (int)((x - base) / nt_b);
     const int64_t pstart = base + (int64_t)hg0 * nt_b;
     const int64_t pend = pstart + nt_b;
-    // Segment bounds, wavefront-uniform by construction; readfirstlane makes
-    // that visible to the compiler, so the loop below keeps uniform branches
-    // (a branch it must treat as divergent gets restructured into paths that
-    // skip loads, which spoils the wait counts of the load pipeline).
-    const int s0 = __builtin_amdgcn_readfirstlane((int)(x - pstart));
-    const int s1 = __builtin_amdgcn_readfirstlane((int)((x1 < pend ? x1 : pend) - pstart));
+    // Segment bounds in real tiles (the pair's first seg_cost positions stand
+    // for its fixed overhead and hold no tiles), wavefront-uniform by
+    // construction; readfirstlane makes that visible to the compiler, so the
+    // loop below keeps uniform branches (a branch it must treat as divergent
+    // gets restructured into paths that skip loads, which spoils the wait
+    // counts of the load pipeline).
+    const int s0 = __builtin_amdgcn_readfirstlane(max((int)(x - pstart) - a.seg_cost, 0));
+    const int s1 = __builtin_amdgcn_readfirstlane(
+        max((int)((x1 < pend ? x1 : pend) - pstart) - a.seg_cost, 0));
     const bool first = s0 == 0;
     const bool last = pend <= x1;
-    const int L = __builtin_amdgcn_readfirstlane(clamped_len(a, b));
-    const int h0 = hg0 * HG;  // first kv head of the group
+    if (s1 > s0) {  // else the range holds only overhead positions of this pair
+      const int L = __builtin_amdgcn_readfirstlane(clamped_len(a, b));
+      const int h0 = hg0 * HG;  // first kv head of the group
 
-    // ---- this wavefront's share of the segment ----
-    f16x8 qf[HG][NC];
-    {
-      const int gq = min(row, a.g - 1);
+      // ---- this wavefront's share of the segment ----
+      f16x8 qf[HG][NC];
+      {
+        const int gq = min(row, a.g - 1);
 #pragma unroll
-      for (int hg = 0; hg < HG; ++hg) {
-        const f16* qp = a.q + (int64_t)b * a.q_sb + (int64_t)((h0 + hg) * a.g + gq) * a.q_sh + grp * 8;
+        for (int hg = 0; hg < HG; ++hg) {
+          const f16* qp = a.q + (int64_t)b * a.q_sb + (int64_t)((h0 + hg) * a.g + gq) * a.q_sh + grp * 8;
 #pragma unroll
-        for (int c = 0; c < NC; ++c) {
-          const f16x8 t = *reinterpret_cast<const f16x8*>(qp + 32 * c);
-          qf[hg][c] = row < a.g ? t : zero8();
-        }
-      }
-    }
-    const int32_t* btrow = a.bt + (int64_t)b * a.bt_sb;
-    const int tok_fallback = s0 * 16;  // a valid token of this segment
-
-    // Natural-layout loads: instruction i of a tile gives lane l the 16-byte
-    // chunk f = 64 i + l of the tile's 16 rows x (HG * D) halves, i.e. row
-    // f / CPR, halves (f % CPR) * 8 of the row's head-group slice. Each
-    // instruction thus reads whole row slices (whole cache lines).
-    auto nat_row = [&](int i) { return (64 * i + lane) / CPR; };
-    auto nat_col = [&](int i) { return ((64 * i + lane) % CPR) * 8; };
-    auto row_token = [&](int ti, int r) {
-      const int t = ti * 16 + r;
-      return (ti < s1 && t < L) ? t : tok_fallback;
-    };
-    auto load_ids = [&](int k, int (&ids)[NT][NID]) {
-#pragma unroll
-      for (int nt = 0; nt < NT; ++nt)
-#pragma unroll
-        for (int j = 0; j < NID; ++j) {
-          const int t = row_token(s0 + k * NT + nt, NID == 1 ? 0 : nat_row(j));
-          if constexpr (UNIFORM_TILE)
-            ids[nt][j] = load_uniform(btrow + (int64_t)blk_of<BS>(t, bs) * a.bt_sk);
-          else
-            ids[nt][j] = btrow[(int64_t)blk_of<BS>(t, bs) * a.bt_sk];
-        }
-    };
-    auto load_kv = [&](int k, const int (&ids)[NT][NID], f16x8 (&kb)[NT][NI], f16x8 (&vb)[NT][NI]) {
-#pragma unroll
-      for (int nt = 0; nt < NT; ++nt) {
-        const int ti = s0 + k * NT + nt;
-        if constexpr (UNIFORM_TILE) {
-          // Unconditional: a tile past the segment gets an empty resource.
-          const int64_t id = min(max(ids[nt][0], 0), a.num_blocks - 1);
-          const int64_t r0 = (ti * 16) % BS;
-          const int nb = ti < s1 ? 0x7fffffff : 0;
-          const auto kr = tile_rsrc(a.k + id * a.k_sb + r0 * a.k_st + (int64_t)h0 * a.k_sh, nb);
-          const auto vr = tile_rsrc(a.v + id * a.v_sb + r0 * a.v_st + (int64_t)h0 * a.v_sh, nb);
-#pragma unroll
-          for (int i = 0; i < NI; ++i) {
-            kb[nt][i] = load_tile(kr, k_lane, (int)(2 * i * RS * a.k_st));
-            vb[nt][i] = load_tile(vr, v_lane, (int)(2 * i * RS * a.v_st));
-          }
-        } else if (ti < s1) {
-#pragma unroll
-          for (int i = 0; i < NI; ++i) {
-            const int t = row_token(ti, nat_row(i));
-            const int64_t id = min(max(ids[nt][NID == 1 ? 0 : i], 0), a.num_blocks - 1);
-            const int64_t off = off_of<BS>(t, bs);
-            const int col = nat_col(i);
-            const int hg = col / D;
-            const int d0 = col - hg * D;
-            kb[nt][i] = load_stream(a.k + id * a.k_sb + off * a.k_st + (int64_t)(h0 + hg) * a.k_sh + d0);
-            vb[nt][i] = load_stream(a.v + id * a.v_sb + off * a.v_st + (int64_t)(h0 + hg) * a.v_sh + d0);
+          for (int c = 0; c < NC; ++c) {
+            const f16x8 t = *reinterpret_cast<const f16x8*>(qp + 32 * c);
+            qf[hg][c] = row < a.g ? t : zero8();
           }
         }
       }
-    };
-    // Writes one tile's rows (natural layout) into the staging buffer laid out
-    // [tile][head][row][LS]; rows past the sequence end are zeroed when asked.
-    auto stage = [&](int k, f16x8 (&buf)[NT][NI], f16* dst, bool zero_tail) {
+      const int32_t* btrow = a.bt + (int64_t)b * a.bt_sb;
+      const int tok_fallback = s0 * 16;  // a valid token of this segment
+
+      // Natural-layout loads: instruction i of a tile gives lane l the 16-byte
+      // chunk f = 64 i + l of the tile's 16 rows x (HG * D) halves, i.e. row
+      // f / CPR, halves (f % CPR) * 8 of the row's head-group slice. Each
+      // instruction thus reads whole row slices (whole cache lines).
+      auto nat_row = [&](int i) { return (64 * i + lane) / CPR; };
+      auto nat_col = [&](int i) { return ((64 * i + lane) % CPR) * 8; };
+      auto row_token = [&](int ti, int r) {
+        const int t = ti * 16 + r;
+        return (ti < s1 && t < L) ? t : tok_fallback;
+      };
+      auto load_ids = [&](int k, int (&ids)[NT][NID]) {
 #pragma unroll
-      for (int nt = 0; nt < NT; ++nt) {
-        const int ti = s0 + k * NT + nt;
-        if (ti < s1) {
+        for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
-          for (int i = 0; i < NI; ++i) {
-            const int r = nat_row(i);
-            const int col = nat_col(i);
-            const int hg = col / D;
-            const int d0 = col - hg * D;
-            *reinterpret_cast<f16x8*>(&dst[((nt * HG + hg) * 16 + r) * LS + d0]) = buf[nt][i];
+          for (int j = 0; j < NID; ++j) {
+            const int t = row_token(s0 + k * NT + nt, NID == 1 ? 0 : nat_row(j));
+            if constexpr (UNIFORM_TILE)
+              ids[nt][j] = load_uniform(btrow + (int64_t)blk_of<BS>(t, bs) * a.bt_sk);
+            else
+              ids[nt][j] = btrow[(int64_t)blk_of<BS>(t, bs) * a.bt_sk];
           }
-          // Rows past the sequence end are overwritten with zeros in LDS (not
-          // selected in registers: a select on freshly loaded registers makes
-          // the compiler wait for those loads where it places the select).
-          if (zero_tail && ti * 16 + 16 > L) {  // wavefront-uniform: the last tile only
+      };
+      auto load_kv = [&](int k, const int (&ids)[NT][NID], u32x4 (&kb)[NT][NI], u32x4 (&vb)[NT][NI]) {
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+          const int ti = s0 + k * NT + nt;
+          if constexpr (UNIFORM_TILE) {
+            // Unconditional: a tile past the segment gets an empty resource.
+            const int64_t id = min(max(ids[nt][0], 0), a.num_blocks - 1);
+            const int64_t r0 = (ti * 16) % BS;
+            const int nb = ti < s1 ? 0x7fffffff : 0;
+            const auto kr = tile_rsrc(a.k + id * a.k_sb + r0 * a.k_st + (int64_t)h0 * a.k_sh, nb);
+            const auto vr = tile_rsrc(a.v + id * a.v_sb + r0 * a.v_st + (int64_t)h0 * a.v_sh, nb);
+#pragma unroll
+            for (int i = 0; i < NI; ++i) {
+              kb[nt][i] = load_tile(kr, k_lane, (int)(2 * i * RS * a.k_st));
+              vb[nt][i] = load_tile(vr, v_lane, (int)(2 * i * RS * a.v_st));
+            }
+          } else if (ti < s1) {
+#pragma unroll
+            for (int i = 0; i < NI; ++i) {
+              const int t = row_token(ti, nat_row(i));
+              const int64_t id = min(max(ids[nt][NID == 1 ? 0 : i], 0), a.num_blocks - 1);
+              const int64_t off = off_of<BS>(t, bs);
+              const int col = nat_col(i);
+              const int hg = col / D;
+              const int d0 = col - hg * D;
+              kb[nt][i] = load_stream(a.k + id * a.k_sb + off * a.k_st + (int64_t)(h0 + hg) * a.k_sh + d0);
+              vb[nt][i] = load_stream(a.v + id * a.v_sb + off * a.v_st + (int64_t)(h0 + hg) * a.v_sh + d0);
+            }
+          }
+        }
+      };
+      // Writes one tile's rows (natural layout) into the staging buffer laid out
+      // [tile][head][row][LS]; rows past the sequence end are zeroed when asked.
+      auto stage = [&](int k, u32x4 (&buf)[NT][NI], f16* dst, bool zero_tail) {
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+          const int ti = s0 + k * NT + nt;
+          if (ti < s1) {
 #pragma unroll
             for (int i = 0; i < NI; ++i) {
               const int r = nat_row(i);
               const int col = nat_col(i);
               const int hg = col / D;
               const int d0 = col - hg * D;
-              if (ti * 16 + r >= L)
-                *reinterpret_cast<f16x8*>(&dst[((nt * HG + hg) * 16 + r) * LS + d0]) = zero8();
+              *reinterpret_cast<u32x4*>(&dst[((nt * HG + hg) * 16 + r) * LS + d0]) = buf[nt][i];
+            }
+            // Rows past the sequence end are overwritten with zeros in LDS (not
+            // selected in registers: a select on freshly loaded registers makes
+            // the compiler wait for those loads where it places the select).
+            if (zero_tail && ti * 16 + 16 > L) {  // wavefront-uniform: the last tile only
+#pragma unroll
+              for (int i = 0; i < NI; ++i) {
+                const int r = nat_row(i);
+                const int col = nat_col(i);
+                const int hg = col / D;
+                const int d0 = col - hg * D;
+                if (ti * 16 + r >= L)
+                  *reinterpret_cast<f16x8*>(&dst[((nt * HG + hg) * 16 + r) * LS + d0]) = zero8();
+              }
             }
           }
         }
-      }
-    };
+      };
 
-    float m_run[HG], l_run[HG];
-    f32x4 acc[HG][ND];
-#pragma unroll
-    for (int hg = 0; hg < HG; ++hg) {
-      m_run[hg] = kNegInf;
-      l_run[hg] = 0.f;
-#pragma unroll
-      for (int i = 0; i < ND; ++i) acc[hg][i] = f32x4{0.f, 0.f, 0.f, 0.f};
-    }
-
-    // Both K and V of chunk k go to LDS first, which frees their registers for
-    // the loads of the chunk two steps ahead; the math then reads LDS only.
-    auto stage_both = [&](int k, f16x8 (&kb)[NT][NI], f16x8 (&vb)[NT][NI]) {
-      stage(k, kb, kst, false);
-      stage(k, vb, vst, true);  // V rows past the sequence end as zeros: 0 * garbage is never NaN
-      wave_lds_fence();
-    };
-    auto compute = [&](int k) {
-      float xs[NT][HG][4];
-      float mloc[HG];
-#pragma unroll
-      for (int hg = 0; hg < HG; ++hg) mloc[hg] = kNegInf;
-#pragma unroll
-      for (int nt = 0; nt < NT; ++nt) {
-        const int ti = s0 + k * NT + nt;
-#pragma unroll
-        for (int hg = 0; hg < HG; ++hg) {
-          if (ti < s1) {
-            const f16* kt = kst + ((nt * HG + hg) * 16 + row) * LS + grp * 8;
-            f32x4 s = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int c = 0; c < NC; ++c)
-              s = __builtin_amdgcn_mfma_f32_16x16x32_f16(*reinterpret_cast<const f16x8*>(kt + 32 * c),
-                                                         qf[hg][c], s, 0, 0, 0);
-            if (ti * 16 + 16 <= L) {  // wavefront-uniform: only the last tile is partial
-#pragma unroll
-              for (int r = 0; r < 4; ++r) xs[nt][hg][r] = s[r] * a.scale_log2;
-            } else {
-#pragma unroll
-              for (int r = 0; r < 4; ++r)
-                xs[nt][hg][r] = ti * 16 + grp * 4 + r < L ? s[r] * a.scale_log2 : kNegInf;
-            }
-#pragma unroll
-            for (int r = 0; r < 4; ++r) mloc[hg] = fmaxf(mloc[hg], xs[nt][hg][r]);
-          } else {
-#pragma unroll
-            for (int r = 0; r < 4; ++r) xs[nt][hg][r] = kNegInf;
-          }
-        }
-      }
+      float m_run[HG], l_run[HG];
+      f32x4 acc[HG][ND];
 #pragma unroll
       for (int hg = 0; hg < HG; ++hg) {
-        float m = mloc[hg];
-        m = fmaxf(m, __shfl_xor(m, 16));
-        m = fmaxf(m, __shfl_xor(m, 32));
-        const float m_new = fmaxf(m_run[hg], m);
-        const float alpha = fast_exp2(m_run[hg] - m_new);
-        l_run[hg] *= alpha;
+        m_run[hg] = kNegInf;
+        l_run[hg] = 0.f;
 #pragma unroll
-        for (int i = 0; i < ND; ++i) acc[hg][i] *= alpha;
-        m_run[hg] = m_new;
+        for (int i = 0; i < ND; ++i) acc[hg][i] = f32x4{0.f, 0.f, 0.f, 0.f};
       }
+
+      // Both K and V of chunk k go to LDS first, which frees their registers for
+      // the loads of the chunk two steps ahead; the math then reads LDS only.
+      auto stage_both = [&](int k, u32x4 (&kb)[NT][NI], u32x4 (&vb)[NT][NI]) {
+        stage(k, kb, kst, false);
+        stage(k, vb, vst, true);  // V rows past the sequence end as zeros: 0 * garbage is never NaN
+        wave_lds_fence();
+      };
+      auto compute = [&](int k) {
+        float xs[NT][HG][4];
+        float mloc[HG];
 #pragma unroll
-      for (int nt = 0; nt < NT; ++nt) {
-        const int ti = s0 + k * NT + nt;
-        if (ti < s1) {
+        for (int hg = 0; hg < HG; ++hg) mloc[hg] = kNegInf;
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+          const int ti = s0 + k * NT + nt;
 #pragma unroll
           for (int hg = 0; hg < HG; ++hg) {
-            f16x4 ph, pl;
+            if (ti < s1) {
+              const f16* kt = kst + ((nt * HG + hg) * 16 + row) * LS + grp * 8;
+              f32x4 s = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              const float pr = fast_exp2(xs[nt][hg][r] - m_run[hg]);
-              l_run[hg] += pr;
-              const f16 hi = (f16)pr;
-              ph[r] = hi;
-              pl[r] = (f16)(pr - (float)hi);
-            }
-            // V^T operand: lane (row, grp) needs V[4 grp + r][16 nd + row], r = 0..3,
-            // which one transposing read of rows 4 grp..4 grp+3 delivers.
-            const f16* vt = vst + ((nt * HG + hg) * 16 + grp * 4 + (row >> 2)) * LS + (row & 3) * 4;
+              for (int c = 0; c < NC; ++c)
+                s = __builtin_amdgcn_mfma_f32_16x16x32_f16(*reinterpret_cast<const f16x8*>(kt + 32 * c),
+                                                           qf[hg][c], s, 0, 0, 0);
+              if (ti * 16 + 16 <= L) {  // wavefront-uniform: only the last tile is partial
 #pragma unroll
-            for (int nd = 0; nd < ND; ++nd) {
-              const f16x4 av = lds_read_tr16(vt + nd * 16);
-              acc[hg][nd] = __builtin_amdgcn_mfma_f32_16x16x16f16(av, ph, acc[hg][nd], 0, 0, 0);
-              acc[hg][nd] = __builtin_amdgcn_mfma_f32_16x16x16f16(av, pl, acc[hg][nd], 0, 0, 0);
+                for (int r = 0; r < 4; ++r) xs[nt][hg][r] = s[r] * a.scale_log2;
+              } else {
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                  xs[nt][hg][r] = ti * 16 + grp * 4 + r < L ? s[r] * a.scale_log2 : kNegInf;
+              }
+#pragma unroll
+              for (int r = 0; r < 4; ++r) mloc[hg] = fmaxf(mloc[hg], xs[nt][hg][r]);
+            } else {
+#pragma unroll
+              for (int r = 0; r < 4; ++r) xs[nt][hg][r] = kNegInf;
             }
           }
         }
-      }
-      wave_lds_fence();
-    };
+#pragma unroll
+        for (int hg = 0; hg < HG; ++hg) {
+          float m = mloc[hg];
+          m = fmaxf(m, __shfl_xor(m, 16));
+          m = fmaxf(m, __shfl_xor(m, 32));
+          const float m_new = fmaxf(m_run[hg], m);
+          const float alpha = fast_exp2(m_run[hg] - m_new);
+          l_run[hg] *= alpha;
+#pragma unroll
+          for (int i = 0; i < ND; ++i) acc[hg][i] *= alpha;
+          m_run[hg] = m_new;
+        }
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+          const int ti = s0 + k * NT + nt;
+          if (ti < s1) {
+#pragma unroll
+            for (int hg = 0; hg < HG; ++hg) {
+              f16x4 ph, pl;
+#pragma unroll
+              for (int r = 0; r < 4; ++r) {
+                const float pr = fast_exp2(xs[nt][hg][r] - m_run[hg]);
+                l_run[hg] += pr;
+                const f16 hi = (f16)pr;
+                ph[r] = hi;
+                pl[r] = (f16)(pr - (float)hi);
+              }
+              // V^T operand: lane (row, grp) needs V[4 grp + r][16 nd + row], r = 0..3,
+              // which one transposing read of rows 4 grp..4 grp+3 delivers.
+              const f16* vt = vst + ((nt * HG + hg) * 16 + grp * 4 + (row >> 2)) * LS + (row & 3) * 4;
+#pragma unroll
+              for (int nd = 0; nd < ND; ++nd) {
+                const f16x4 av = lds_read_tr16(vt + nd * 16);
+                acc[hg][nd] = __builtin_amdgcn_mfma_f32_16x16x16f16(av, ph, acc[hg][nd], 0, 0, 0);
+                acc[hg][nd] = __builtin_amdgcn_mfma_f32_16x16x16f16(av, pl, acc[hg][nd], 0, 0, 0);
+              }
+            }
+          }
+        }
+        wave_lds_fence();
+      };
 
-    // Wavefront-local pipeline over its chunks k = wave, wave + NW, ... (step
-    // s = 0, 1, ...): K/V register sets Y0/Y1 hold steps s and s+1, id sets
-    // X0/X1 hold the block ids two and three steps ahead. At step s: stage
-    // Y[s%2] into LDS, reuse it for the loads of step s+2 (ids in X[s%2]),
-    // fetch the ids of step s+3 into X[(s+1)%2], then compute step s.
-    const int nck = __builtin_amdgcn_readfirstlane((s1 - s0 + NT - 1) / NT);
-    if (wave < nck) {
-      f16x8 kb0[NT][NI], vb0[NT][NI], kb1[NT][NI], vb1[NT][NI];
-      int ids0[NT][NID], ids1[NT][NID];
-      // Loads of chunks past the segment are issued anyway (empty resources,
+      // Wavefront-local pipeline over the chunks this wavefront claims. The
+      // wavefronts of the workgroup claim the segment's chunks one at a time
+      // from an LDS counter, so a wavefront that runs faster (the hardware
+      // favours older wavefronts) takes more of them and all finish together.
+      // Step s computes chunk c_s: K/V register sets Y0/Y1 hold steps s and
+      // s+1, id sets X0/X1 the block ids of steps s+2 and s+3. At step s: stage
+      // Y[s%2] into LDS, reuse it for the loads of step s+2 (ids in X[s%2]),
+      // claim step s+3 and fetch its ids into X[(s+1)%2], then compute step s.
+      // Claims are increasing per wavefront, so the first claim past the end
+      // ends its work; loads of such chunks are issued anyway (empty resources,
       // clamped table reads) so that no branch separates them.
-      const int c0 = wave;
-      load_ids(c0, ids0);
-      load_ids(c0 + NW, ids1);
-      load_kv(c0, ids0, kb0, vb0);
-      load_kv(c0 + NW, ids1, kb1, vb1);
-      load_ids(c0 + 2 * NW, ids0);
-      // Two steps per trip, one exit: both steps issue their loads on every
-      // trip and only the LDS staging and the math of a step past the end are
-      // skipped, so every path through the loop issues the same loads.
-      for (int k = c0; k < nck; k += 2 * NW) {
-        stage_both(k, kb0, vb0);
-        load_kv(k + 2 * NW, ids0, kb0, vb0);
-        load_ids(k + 3 * NW, ids1);
-        compute(k);
-        const bool more = k + NW < nck;
-        if (more) stage_both(k + NW, kb1, vb1);
-        load_kv(k + 3 * NW, ids1, kb1, vb1);
-        load_ids(k + 4 * NW, ids0);
-        if (more) compute(k + NW);
-      }
-    }
-
-    // ---- merge the wavefronts' states through LDS ----
-    // Every wavefront stores its maxima and denominators per head and its
-    // accumulators in register layout (chunk j = hg * ND + nd: one f32x4 per
-    // lane, so the 16-byte LDS writes are conflict-free). Wavefront w then
-    // combines chunks j = w, w + NW, ... of all wavefronts and stores them.
-    float* cm = reinterpret_cast<float*>(my_smem);
-    __syncthreads();  // every wavefront is done with its staging buffers
-#pragma unroll
-    for (int hg = 0; hg < HG; ++hg) {
-      float l = l_run[hg];
-      l += __shfl_xor(l, 16);
-      l += __shfl_xor(l, 32);
-      if (grp == 0) {
-        cm[hg * 16 + row] = m_run[hg];
-        cm[HG * 16 + hg * 16 + row] = l;
-      }
-#pragma unroll
-      for (int nd = 0; nd < ND; ++nd)
-        *reinterpret_cast<f32x4*>(&cm[32 * HG + ((hg * ND + nd) * 64 + lane) * 4]) = acc[hg][nd];
-    }
-    __syncthreads();
-    for (int j = wave; j < HG * ND; j += NW) {
-      const int hg = j / ND;
-      const int nd = j - hg * ND;
-      float mw[NW];
-      float M = kNegInf;
-#pragma unroll
-      for (int w = 0; w < NW; ++w) {
-        mw[w] = reinterpret_cast<const float*>(smem + w * WAVE_BYTES)[hg * 16 + row];
-        M = fmaxf(M, mw[w]);
-      }
-      float den = 0.f;
-      f32x4 num = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int w = 0; w < NW; ++w) {
-        const float* c = reinterpret_cast<const float*>(smem + w * WAVE_BYTES);
-        const float sc = mw[w] == kNegInf ? 0.f : fast_exp2(mw[w] - M);
-        den += sc * c[HG * 16 + hg * 16 + row];
-        num += sc * *reinterpret_cast<const f32x4*>(&c[32 * HG + (j * 64 + lane) * 4]);
-      }
-      if (row < a.g) {
-        if (first && last) {
-          const float inv = den > 0.f ? 1.f / den : 0.f;
-          f16x4 o;
-#pragma unroll
-          for (int r = 0; r < 4; ++r) o[r] = (f16)(num[r] * inv);
-          *reinterpret_cast<f16x4*>(a.out + (int64_t)b * a.o_sb +
-                                    (int64_t)((h0 + hg) * a.g + row) * a.o_sh + nd * 16 + grp * 4) = o;
-        } else {
-          float* rec = a.recs + ((int64_t)(wg * 2 + (first ? 1 : 0)) * HG + hg) * REC;
-          if (grp == 0 && nd == 0) {
-            rec[row] = M;
-            rec[16 + row] = den;
-          }
-          *reinterpret_cast<f32x4*>(&rec[32 + row * D + nd * 16 + grp * 4]) = num;
+      const int nck = __builtin_amdgcn_readfirstlane((s1 - s0 + NT - 1) / NT);
+      auto claim = [&]() {
+        int c = 0;
+        if (lane == 0) c = __hip_atomic_fetch_add(&s_next, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        return __builtin_amdgcn_readfirstlane(c);
+      };
+      {
+        u32x4 kb0[NT][NI], vb0[NT][NI], kb1[NT][NI], vb1[NT][NI];
+        int ids0[NT][NID], ids1[NT][NID];
+        int c0 = claim();
+        int c1 = claim();
+        int c2 = claim();
+        load_ids(c0, ids0);
+        load_ids(c1, ids1);
+        // The scheduler must keep the loads of step 0 ahead of those of step 1:
+        // the loop's waits count on the older buffer being the one staged first.
+        load_kv(c0, ids0, kb0, vb0);
+        __builtin_amdgcn_sched_barrier(0);
+        load_kv(c1, ids1, kb1, vb1);
+        __builtin_amdgcn_sched_barrier(0);
+        load_ids(c2, ids0);
+        // Two steps per trip, one exit: both steps issue their loads on every
+        // trip and only the LDS staging and the math of a step past the end are
+        // skipped, so every path through the loop issues the same loads.
+        while (c0 < nck) {
+          stage_both(c0, kb0, vb0);
+          load_kv(c2, ids0, kb0, vb0);
+          const int c3 = claim();
+          load_ids(c3, ids1);
+          compute(c0);
+          const bool more = c1 < nck;
+          if (more) stage_both(c1, kb1, vb1);
+          load_kv(c3, ids1, kb1, vb1);
+          const int c4 = claim();
+          load_ids(c4, ids0);
+          if (more) compute(c1);
+          c0 = c2;
+          c1 = c3;
+          c2 = c4;
         }
       }
-    }
-    __syncthreads();  // the merge state aliases the staging buffers of the next segment
 
+      // ---- merge the wavefronts' states through LDS ----
+      // Every wavefront stores its maxima and denominators per head and its
+      // accumulators in register layout (chunk j = hg * ND + nd: one f32x4 per
+      // lane, so the 16-byte LDS writes are conflict-free). Wavefront w then
+      // combines chunks j = w, w + NW, ... of all wavefronts and stores them.
+      float* cm = reinterpret_cast<float*>(my_smem);
+      __syncthreads();  // every wavefront is done with its staging buffers and its claims
+      if (tid == 0) s_next = 0;  // published to the next segment by the barriers below
+#pragma unroll
+      for (int hg = 0; hg < HG; ++hg) {
+        float l = l_run[hg];
+        l += __shfl_xor(l, 16);
+        l += __shfl_xor(l, 32);
+        if (grp == 0) {
+          cm[hg * 16 + row] = m_run[hg];
+          cm[HG * 16 + hg * 16 + row] = l;
+        }
+#pragma unroll
+        for (int nd = 0; nd < ND; ++nd)
+          *reinterpret_cast<f32x4*>(&cm[32 * HG + ((hg * ND + nd) * 64 + lane) * 4]) = acc[hg][nd];
+      }
+      __syncthreads();
+      for (int j = wave; j < HG * ND; j += NW) {
+        const int hg = j / ND;
+        const int nd = j - hg * ND;
+        float mw[NW];
+        float M = kNegInf;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) {
+          mw[w] = reinterpret_cast<const float*>(smem + w * WAVE_BYTES)[hg * 16 + row];
+          M = fmaxf(M, mw[w]);
+        }
+        float den = 0.f;
+        f32x4 num = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int w = 0; w < NW; ++w) {
+          const float* c = reinterpret_cast<const float*>(smem + w * WAVE_BYTES);
+          const float sc = mw[w] == kNegInf ? 0.f : fast_exp2(mw[w] - M);
+          den += sc * c[HG * 16 + hg * 16 + row];
+          num += sc * *reinterpret_cast<const f32x4*>(&c[32 * HG + (j * 64 + lane) * 4]);
+        }
+        if (row < a.g) {
+          if (first && last) {
+            const float inv = den > 0.f ? 1.f / den : 0.f;
+            f16x4 o;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) o[r] = (f16)(num[r] * inv);
+            *reinterpret_cast<f16x4*>(a.out + (int64_t)b * a.o_sb +
+                                      (int64_t)((h0 + hg) * a.g + row) * a.o_sh + nd * 16 + grp * 4) = o;
+          } else {
+            float* rec = a.recs + ((int64_t)(wg * 2 + (first ? 1 : 0)) * HG + hg) * REC;
+            if (grp == 0 && nd == 0) {
+              rec[row] = M;
+              rec[16 + row] = den;
+            }
+            *reinterpret_cast<f32x4*>(&rec[32 + row * D + nd * 16 + grp * 4]) = num;
+          }
+        }
+      }
+      __syncthreads();  // the merge state aliases the staging buffers of the next segment
+    }
     x = pend;
     if (x < x_end && x >= (int64_t)NHG * s_pref[b + 1]) {
       ++b;
@@ -583,11 +619,12 @@ __global__ __launch_bounds__(1024) void merge_streamk_kernel(DecodeArgs a) {
   const int b = p / NHG;
   const int hgp = p - b * NHG;
   const int sb = a.pref[b];
-  const int nt = a.pref[b + 1] - sb;
-  if (nt == 0) return;
+  const int width = a.pref[b + 1] - sb;  // pair width: seg_cost + tiles
+  if (width == 0) return;
+  const int nt = width - a.seg_cost;
   const int64_t T = (int64_t)NHG * a.pref[a.num_seqs];
   const int G = (int)(T < a.num_wg ? T : a.num_wg);
-  const int64_t pstart = (int64_t)NHG * sb + (int64_t)hgp * nt;
+  const int64_t pstart = (int64_t)NHG * sb + (int64_t)hgp * width + a.seg_cost;  // first tile
   const int wa = wg_of(pstart, T, G);
   const int wb = wg_of(pstart + nt - 1, T, G);
   if (wa == wb) return;
@@ -636,7 +673,7 @@ __global__ __launch_bounds__(1024) void merge_streamk_kernel(DecodeArgs a) {
 // ---------------------------------------------------------------------------
 namespace {
 
-constexpr int kSkWaves = 4;
+constexpr int kSkWaves = 8;
 
 // Tiles per chunk: two chunks of K/V (one computing, one in flight) must fit
 // the 256 VGPRs a wavefront has at two wavefronts per SIMD.
