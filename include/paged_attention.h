@@ -7,6 +7,13 @@
  * caller through `workspace`, sized by the matching *_workspace_bytes() call.
  * Every launch is asynchronous on the given stream; nothing synchronises the host.
  *
+ * Workspace of pa_decode_batched_f16 / pa_decode_v2_f16: its first bytes hold
+ * per-(sequence, kv-head group) arrival counters of the in-kernel merge of
+ * split partitions. They must be zero before the first call that uses the
+ * buffer (zero-fill it once after allocating); every call leaves them zero
+ * again. Use one such buffer per stream (calls in flight on different streams
+ * must not share one) and lend it to nothing else, pa_decode_v1_f16 included.
+ *
  * Tensor layouts (element strides, fp16 = IEEE binary16):
  *   q        [num_seqs, num_q_heads, head_dim]            stride of head_dim must be 1
  *   k_cache  [num_blocks, block_size, num_kv_heads, head_dim]  (same for v_cache)
@@ -41,7 +48,8 @@ enum {
   PA_ERR_HIP = 4           /* the HIP runtime reported an error at launch */
 };
 
-/* ABI revision of this header; bumps whenever a signature changes. */
+/* ABI revision of this header; bumps whenever a signature or a workspace
+ * contract changes (2: zero-initialised decode workspace). */
 PA_API int pa_abi_version(void);
 
 /* Message of the last failed call on this thread ("" after a success). */

@@ -40,15 +40,17 @@ def test_abi_version():
 def test_workspace_sizes():
     lib = _native.load()
     rec = (32 + 16 * 64) * 4
-    # Stream-K (<= 1024 sequences): 2 records per workgroup of the grid bound, each
-    # covering the kv heads one wavefront handles (2 at head_dim 64), then the
-    # per-sequence tile prefix. The bound is the tile count when that is smaller.
-    assert lib.pa_decode_batched_workspace_bytes(8, 14, 2, 64, 16, 32) == 256 * 2 * 2 * rec + 9 * 4
-    assert lib.pa_decode_batched_workspace_bytes(256, 14, 2, 64, 16, 2048) == 1024 * 2 * 2 * rec + 257 * 4
+    counters = 65536 * 4  # per-pair arrival counters at the start of every decode workspace
+    # Stream-K (<= 1024 sequences): the counters, then 2 records per workgroup of the
+    # grid bound, each covering the kv heads one wavefront handles (2 at head_dim 64).
+    # The bound is the tile count when that is smaller.
+    assert lib.pa_decode_batched_workspace_bytes(8, 14, 2, 64, 16, 32) == counters + 256 * 2 * 2 * rec
+    assert lib.pa_decode_batched_workspace_bytes(256, 14, 2, 64, 16, 2048) == counters + 1024 * 2 * 2 * rec
     rec128 = (32 + 16 * 128) * 4
-    assert lib.pa_decode_batched_workspace_bytes(64, 28, 7, 128, 16, 128) == 1024 * 2 * rec128 + 65 * 4
-    # Fixed-split path beyond 1024 sequences: 2048-block rows -> 64 splits of 512 tokens.
-    assert lib.pa_decode_batched_workspace_bytes(2000, 14, 2, 64, 16, 2048) == 2000 * 2 * 64 * rec
+    assert lib.pa_decode_batched_workspace_bytes(64, 28, 7, 128, 16, 128) == counters + 1024 * 2 * rec128
+    # Fixed-split path beyond 1024 sequences: 2048-block rows -> 64 splits of 512 tokens,
+    # placed after the counter region so one buffer serves both paths.
+    assert lib.pa_decode_batched_workspace_bytes(2000, 14, 2, 64, 16, 2048) == counters + 2000 * 2 * 64 * rec
     assert lib.pa_decode_batched_workspace_bytes(2000, 14, 2, 64, 16, 32) == 0
     assert lib.pa_decode_v1_workspace_bytes(14, 2, 64, 16, 67) == 2 * 16 * 80 * 4
     assert lib.pa_decode_batched_workspace_bytes(8, 14, 2, 48, 16, 2048) == 0  # unsupported dim

@@ -257,3 +257,42 @@ def test_large_batch_fixed_split_path(cuda_device, d):
     err = max_err(out[seqs], oracle32(q, k, v, tables, ls, w.scale))
     print(f"[parity] fixed-split path D{d}: max abs err {err:.3e}", flush=True)
     assert err <= TOL
+
+
+def _decode_counters(device):
+    """The pair-counter region (first 256 KB) of this stream's decode workspace."""
+    from engine.kernels import _native
+
+    key = (device.index, torch.cuda.current_stream(device).cuda_stream, _native.WS_DECODE)
+    return _native._workspaces[key][:65536 * 4].view(torch.int32)
+
+
+def test_merge_counters_return_to_zero(cuda_device):
+    """Every call leaves the in-kernel merge counters at zero (the next call relies on it)."""
+    w = workloads.long_context(device=cuda_device, seed=3, num_seqs=64)
+    first = None
+    for _ in range(3):
+        out = paged_attention_decode_batched(w.q, w.k_cache, w.v_cache, w.block_tables,
+                                             w.seq_lens, w.scale)
+        torch.cuda.synchronize()
+        assert torch.count_nonzero(_decode_counters(cuda_device)).item() == 0
+        first = out if first is None else first
+        assert max_err(out, first.float().cpu()) <= TOL
+    _check_workload(w, seqs=[0, 1, 7, 8, 31, 63])
+
+
+def test_paths_interleaved_on_one_stream(cuda_device):
+    """Stream-K, fixed-split and two-pass calls alternate on one stream without
+    disturbing each other's scratch: each result still matches the oracle."""
+    a = workloads.long_context(device=cuda_device, seed=4, num_seqs=32)
+    rng = np.random.default_rng(11)
+    lens = rng.integers(1, 900, size=1030).tolist()
+    big = workloads.make_random(len(lens), 14, 2, 64, lens, 16, seed=12, device=cuda_device)
+    q1, kc, vc, bt, ids = reference_style_case(14, 2, 64, 16, 777, 13, cuda_device)
+    for _ in range(2):
+        _check_workload(a, seqs=[0, 5, 9, 31])
+        _check_workload(big, seqs=[0, 1, 515, 1029])
+        got = paged_attention_decode_v1(q1, kc, vc, bt, 777, 0.125)
+        want = oracle32(q1[None], kc, vc, [ids], [777], 0.125)[0]
+        assert max_err(got, want) <= TOL
+        assert torch.count_nonzero(_decode_counters(cuda_device)).item() == 0

@@ -113,10 +113,19 @@ static size_t streamk_records_bytes(int num_kv_heads, int head_dim, int grid) {
   return (size_t)grid * 2 * hg * record_floats(head_dim) * sizeof(float);
 }
 
+// Stream-K workspace: the pair counters (kSkCounterBytes, zero between
+// launches) followed by the partial records.
 static size_t streamk_workspace(int num_seqs, int num_kv_heads, int head_dim, int block_size,
                                 int max_blocks) {
   const int grid = streamk_grid_bound(num_seqs, num_kv_heads, head_dim, block_size, max_blocks);
-  return streamk_records_bytes(num_kv_heads, head_dim, grid) + (size_t)(num_seqs + 1) * sizeof(int);
+  return kSkCounterBytes + streamk_records_bytes(num_kv_heads, head_dim, grid);
+}
+
+// The stream-K plan holds up to kSkMaxSeqs sequences in LDS and counts
+// arrivals for up to kSkMaxPairs (sequence, kv-head group) pairs.
+static bool streamk_ok(int num_seqs, int num_kv_heads, int head_dim) {
+  const int hg = streamk_head_group(num_kv_heads, head_dim);
+  return num_seqs <= kSkMaxSeqs && (int64_t)(num_kv_heads / hg) * num_seqs <= kSkMaxPairs;
 }
 
 // Compute units of the current device (cached per device).
@@ -133,7 +142,8 @@ static int device_cus() {
   return cache[dev];
 }
 
-// Fills the stream-K fields of `a` and launches; `ws` holds the records then the prefix.
+// Fills the stream-K fields of `a` and launches; `ws` holds the pair counters
+// then the records.
 static hipError_t launch_streamk_with(DecodeArgs& a, int num_seqs, int head_dim, void* ws,
                                       hipStream_t s) {
   const int bound = streamk_grid_bound(num_seqs, a.hkv, head_dim, a.bs, a.max_blocks);
@@ -144,8 +154,8 @@ static hipError_t launch_streamk_with(DecodeArgs& a, int num_seqs, int head_dim,
   // (measured on MI355X: pipeline fill plus the merge across wavefronts).
   const int tile_bytes = 64 * streamk_head_group(a.hkv, head_dim) * head_dim;
   a.seg_cost = (160 << 10) / tile_bytes;
-  a.recs = (float*)ws;
-  a.pref = (int*)((char*)ws + streamk_records_bytes(a.hkv, head_dim, bound));
+  a.cnt = (int*)ws;
+  a.recs = (float*)((char*)ws + kSkCounterBytes);
   return launch_decode_streamk(a, head_dim, s);
 }
 
@@ -155,7 +165,7 @@ using namespace pa;
 
 extern "C" {
 
-int pa_abi_version(void) { return 1; }
+int pa_abi_version(void) { return 2; }
 
 const char* pa_last_error(void) { return g_error.c_str(); }
 
@@ -165,12 +175,14 @@ size_t pa_decode_batched_workspace_bytes(int num_seqs, int num_q_heads, int num_
   if (num_seqs <= 0 || num_kv_heads <= 0 || block_size <= 0 || max_blocks_per_seq <= 0 ||
       !supported_head_dim(head_dim))
     return 0;
-  if (num_seqs <= kSkMaxSeqs)
+  if (streamk_ok(num_seqs, num_kv_heads, head_dim))
     return streamk_workspace(num_seqs, num_kv_heads, head_dim, block_size, max_blocks_per_seq);
+  // The fixed-split records start after the counter region too, so that one
+  // workspace can serve both paths without touching the stream-K counters.
   const int st = split_tiles_for(kSplitTilesBatched, block_size);
   const int64_t ms = splits_for(max_tiles_for(max_blocks_per_seq, block_size), st);
   if (ms <= 1) return 0;
-  return (size_t)num_seqs * num_kv_heads * ms * record_floats(head_dim) * sizeof(float);
+  return kSkCounterBytes + (size_t)num_seqs * num_kv_heads * ms * record_floats(head_dim) * sizeof(float);
 }
 
 int pa_decode_batched_f16(const void* q, const int64_t q_strides[3], const void* k_cache,
@@ -236,7 +248,7 @@ int pa_decode_batched_f16(const void* q, const int64_t q_strides[3], const void*
   a.out = (f16*)out;
   a.o_sb = out_strides[0];
   a.o_sh = out_strides[1];
-  a.ws = (float*)workspace;
+  a.ws = workspace ? (float*)((char*)workspace + kSkCounterBytes) : nullptr;
   a.hkv = num_kv_heads;
   a.g = num_q_heads / num_kv_heads;
   a.bs = block_size;
@@ -245,7 +257,7 @@ int pa_decode_batched_f16(const void* q, const int64_t q_strides[3], const void*
   a.split_tiles = st;
   a.max_splits = (int)ms;
   a.scale_log2 = scale * kLog2e;
-  if (num_seqs <= kSkMaxSeqs)
+  if (streamk_ok(num_seqs, num_kv_heads, head_dim))
     return finish_launch(launch_streamk_with(a, num_seqs, head_dim, workspace, (hipStream_t)stream));
   return finish_launch(launch_decode_split(a, head_dim, num_seqs, (hipStream_t)stream));
 }

@@ -40,20 +40,23 @@ struct DecodeArgs {
   int split_tiles, max_splits;
   int lpad;  // v1: padded score-row length
   float scale_log2;  // softmax scale times log2(e): scores live in the exp2 domain
-  // Stream-K schedule (decode_streamk_kernel / merge_streamk_kernel).
+  // Stream-K schedule (decode_streamk_kernel).
   int num_seqs;  // sequences in the batch
   int num_wg;    // workgroups of the persistent grid
   float* recs;   // 2 partial records per workgroup
-  int* pref;     // per-sequence exclusive prefix of pair widths, num_seqs + 1 entries
+  int* cnt;      // per-pair arrival counters, zero between launches
   // Fixed cost of a pair segment (pipeline fill, cross-wavefront merge),
   // in tiles: the schedule splits tiles plus this cost per pair evenly.
   int seg_cost;
 };
 
-// Stream-K limits: sequences whose tile prefix fits the LDS plan, and the
-// largest persistent grid the workspace is sized for.
+// Stream-K limits: sequences whose tile prefix fits the LDS plan, the largest
+// persistent grid the workspace is sized for, and the (sequence, kv-head
+// group) pairs the counter region at the start of the workspace holds.
 constexpr int kSkMaxSeqs = 1024;
 constexpr int kSkMaxWG = 1024;
+constexpr int kSkMaxPairs = 65536;
+constexpr size_t kSkCounterBytes = (size_t)kSkMaxPairs * sizeof(int);
 // Persistent workgroups per compute unit (each of eight wavefronts).
 constexpr int kSkWgPerCu = 1;
 

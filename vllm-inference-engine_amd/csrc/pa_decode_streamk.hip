@@ -81,6 +81,17 @@ __device__ inline f16x4 lds_read_tr16(const f16* p) {
   return __builtin_bit_cast(f16x4, __builtin_amdgcn_ds_read_tr16_b64_v4f16(lp));
 }
 
+// Partial records cross XCDs (each has its own L2): they are written and read
+// with device-coherent accesses (agent-scope atomic stores and loads: sc1
+// write-through / coherent-miss), so publishing one needs no L2 writeback or
+// invalidate -- fences that would stall the whole XCD's L2 mid-kernel.
+__device__ inline void store_coherent(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ inline float load_coherent(const float* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // Read of a table entry at a wavefront-uniform address through the scalar
 // data cache (s_load): the block tables and lengths are never written by
 // these kernels, and scalar loads are counted apart from the vector loads, so
@@ -108,6 +119,55 @@ __host__ __device__ inline int wg_of(int64_t x, int64_t T, int G) {
 
 __host__ __device__ inline int64_t range_start(int w, int64_t T, int G) {
   return (int64_t)w * T / G;
+}
+
+// Combines the partial records of one pair cut by workgroup range
+// boundaries: records of ranges wa..wa+nrec-1 (wa's tail slot, the others'
+// head slots), read eight at a time with every load issued before any is
+// used (device-coherent loads: the records were written on other XCDs) and
+// folded in by an online log-sum-exp. One output element per thread
+// of the calling workgroup (nthr threads).
+template <int D, int HG>
+__device__ void merge_records(const DecodeArgs& a, int b, int hgp, int wa, int nrec, int tid, int nthr) {
+  constexpr int REC = record_floats(D);
+  constexpr int BATCH = 8;
+  const int nout = HG * a.g * D;
+  for (int i = tid; i < nout; i += nthr) {
+    const int hg = i / (a.g * D);
+    const int rem = i - hg * a.g * D;
+    const int hd = rem / D;
+    const int d = rem - hd * D;
+    float M = kNegInf, num = 0.f, den = 0.f;
+    for (int k0 = 0; k0 < nrec; k0 += BATCH) {
+      float mv[BATCH], lv[BATCH], av[BATCH];
+#pragma unroll
+      for (int j = 0; j < BATCH; ++j) {
+        const int k = k0 + j;
+        const int kk = k < nrec ? k : 0;
+        const int slot = 2 * (wa + kk) + (kk == 0 ? 1 : 0);
+        const float* r = a.recs + ((int64_t)slot * HG + hg) * REC;
+        mv[j] = load_coherent(r + hd);
+        lv[j] = load_coherent(r + 16 + hd);
+        av[j] = load_coherent(r + 32 + hd * D + d);
+        if (k >= nrec) mv[j] = kNegInf;
+      }
+      float mb = M;
+#pragma unroll
+      for (int j = 0; j < BATCH; ++j) mb = fmaxf(mb, mv[j]);
+      const float sc = M == kNegInf ? 0.f : fast_exp2(M - mb);
+      num *= sc;
+      den *= sc;
+#pragma unroll
+      for (int j = 0; j < BATCH; ++j) {
+        const float w = mv[j] == kNegInf ? 0.f : fast_exp2(mv[j] - mb);
+        num += w * av[j];
+        den += w * lv[j];
+      }
+      M = mb;
+    }
+    a.out[(int64_t)b * a.o_sb + (int64_t)((hgp * HG + hg) * a.g + hd) * a.o_sh + d] =
+        (f16)(den > 0.f ? num / den : 0.f);
+  }
 }
 
 template <int D, int NT, int BS, int HG, int NW>
@@ -139,6 +199,7 @@ void decode_streamk_kernel(DecodeArgs a) {
   __shared__ int s_pref[kSkMaxSeqs + 1];
   __shared__ int s_wtot[NW];
   __shared__ int s_next;  // next unclaimed chunk of the current segment
+  __shared__ int s_merge[2];  // pairs this workgroup completes (-1: none)
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -197,9 +258,6 @@ void decode_streamk_kernel(DecodeArgs a) {
       s_next = 0;
     }
     __syncthreads();
-  }
-  if (wg == 0 && a.pref) {
-    for (int b = tid; b <= B; b += NTHR) a.pref[b] = s_pref[b];
   }
 
   // Zero-length sequences have no tiles; their rows are written as zeros.
@@ -261,6 +319,12 @@ void decode_streamk_kernel(DecodeArgs a) {
     ++b;
     while (b < B - 1 && s_pref[b + 1] == s_pref[b]) ++b;
   }
+
+  // Pairs this workgroup left a partial record for (at most two: the pair it
+  // continues from the previous range and the pair cut at its range end), and
+  // the counter values its arrivals returned; read after the last segment.
+  int pend_pair[2] = {-1, -1};
+  int pend_old[2] = {0, 0};
 
   for (int pass = 0; pass < 2; ++pass) {
   int64_t x = pass == 0 ? cont_end : x0;
@@ -587,11 +651,26 @@ void decode_streamk_kernel(DecodeArgs a) {
           } else {
             float* rec = a.recs + ((int64_t)(wg * 2 + (first ? 1 : 0)) * HG + hg) * REC;
             if (grp == 0 && nd == 0) {
-              rec[row] = M;
-              rec[16 + row] = den;
+              store_coherent(&rec[row], M);
+              store_coherent(&rec[16 + row], den);
             }
-            *reinterpret_cast<f32x4*>(&rec[32 + row * D + nd * 16 + grp * 4]) = num;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) store_coherent(&rec[32 + row * D + nd * 16 + grp * 4 + r], num[r]);
           }
+        }
+      }
+      if (!(first && last)) {
+        // Publish the record: every thread waits for its coherent stores to
+        // complete, then one arrival is counted for the pair. The returned
+        // count is only needed after the last segment, so the atomic's latency
+        // overlaps the rest of the range.
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        if (tid == 0) {
+          const int slot = first ? 1 : 0;
+          pend_pair[slot] = b * NHG + hg0;
+          pend_old[slot] = __hip_atomic_fetch_add(a.cnt + b * NHG + hg0, 1, __ATOMIC_RELAXED,
+                                                  __HIP_MEMORY_SCOPE_AGENT);
         }
       }
       __syncthreads();  // the merge state aliases the staging buffers of the next segment
@@ -603,68 +682,40 @@ void decode_streamk_kernel(DecodeArgs a) {
     }
   }
   }
-}
 
-// Combines the partial records of pairs cut by workgroup range boundaries.
-// One workgroup per pair, one thread per output element. The pair's records
-// are those of workgroups wa..wb (wa's tail slot, the others' head slots);
-// they are read eight at a time with every load issued before any is used,
-// and folded in with an online log-sum-exp.
-template <int D, int HG>
-__global__ __launch_bounds__(1024) void merge_streamk_kernel(DecodeArgs a) {
-  constexpr int REC = record_floats(D);
-  constexpr int BATCH = 8;
-  const int NHG = a.hkv / HG;
-  const int p = blockIdx.x;
-  const int b = p / NHG;
-  const int hgp = p - b * NHG;
-  const int sb = a.pref[b];
-  const int width = a.pref[b + 1] - sb;  // pair width: seg_cost + tiles
-  if (width == 0) return;
-  const int nt = width - a.seg_cost;
-  const int64_t T = (int64_t)NHG * a.pref[a.num_seqs];
-  const int G = (int)(T < a.num_wg ? T : a.num_wg);
-  const int64_t pstart = (int64_t)NHG * sb + (int64_t)hgp * width + a.seg_cost;  // first tile
-  const int wa = wg_of(pstart, T, G);
-  const int wb = wg_of(pstart + nt - 1, T, G);
-  if (wa == wb) return;
-  const int nrec = wb - wa + 1;
-  const int nout = HG * a.g * D;
-  for (int i = threadIdx.x; i < nout; i += blockDim.x) {
-    const int hg = i / (a.g * D);
-    const int rem = i - hg * a.g * D;
-    const int hd = rem / D;
-    const int d = rem - hd * D;
-    float M = kNegInf, num = 0.f, den = 0.f;
-    for (int k0 = 0; k0 < nrec; k0 += BATCH) {
-      float mv[BATCH], lv[BATCH], av[BATCH];
+  // ---- pairs cut by range boundaries: the last workgroup to arrive merges ----
+  // A pair spanning ranges wa..wb has one record per range (wa's tail slot,
+  // the others' head slots). The workgroup whose arrival completes the count
+  // combines them by log-sum-exp and resets the counter to zero for the next
+  // launch, so the counters stay zero between launches.
+  if (tid == 0) {
 #pragma unroll
-      for (int j = 0; j < BATCH; ++j) {
-        const int k = k0 + j;
-        const int kk = k < nrec ? k : 0;
-        const int slot = 2 * (wa + kk) + (kk == 0 ? 1 : 0);
-        const float* r = a.recs + ((int64_t)slot * HG + hg) * REC;
-        mv[j] = r[hd];
-        lv[j] = r[16 + hd];
-        av[j] = r[32 + hd * D + d];
-        if (k >= nrec) mv[j] = kNegInf;
+    for (int k = 0; k < 2; ++k) {
+      int m = -1;
+      if (pend_pair[k] >= 0) {
+        const int p = pend_pair[k];
+        const int pb = p / NHG;
+        const int nt = s_pref[pb + 1] - s_pref[pb] - a.seg_cost;
+        const int64_t ps = (int64_t)NHG * s_pref[pb] + (int64_t)(p - pb * NHG) * (nt + a.seg_cost) + a.seg_cost;
+        const int need = wg_of(ps + nt - 1, T, Ge) - wg_of(ps, T, Ge) + 1;
+        if (pend_old[k] == need - 1) m = p;
       }
-      float mb = M;
-#pragma unroll
-      for (int j = 0; j < BATCH; ++j) mb = fmaxf(mb, mv[j]);
-      const float sc = M == kNegInf ? 0.f : fast_exp2(M - mb);
-      num *= sc;
-      den *= sc;
-#pragma unroll
-      for (int j = 0; j < BATCH; ++j) {
-        const float w = mv[j] == kNegInf ? 0.f : fast_exp2(mv[j] - mb);
-        num += w * av[j];
-        den += w * lv[j];
-      }
-      M = mb;
+      s_merge[k] = m;
     }
-    a.out[(int64_t)b * a.o_sb + (int64_t)((hgp * HG + hg) * a.g + hd) * a.o_sh + d] =
-        (f16)(den > 0.f ? num / den : 0.f);
+  }
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const int p = s_merge[k];
+    if (p < 0) continue;
+    const int pb = p / NHG;
+    const int hgp = p - pb * NHG;
+    const int nt = s_pref[pb + 1] - s_pref[pb] - a.seg_cost;
+    const int64_t ps = (int64_t)NHG * s_pref[pb] + (int64_t)hgp * (nt + a.seg_cost) + a.seg_cost;
+    const int wa = wg_of(ps, T, Ge);
+    const int nrec = wg_of(ps + nt - 1, T, Ge) - wa + 1;
+    merge_records<D, HG>(a, pb, hgp, wa, nrec, tid, NTHR);
+    if (tid == 0) __hip_atomic_store(a.cnt + p, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
@@ -686,8 +737,6 @@ template <int D, int BS, int HG>
 hipError_t launch_sk(const DecodeArgs& a, hipStream_t s) {
   constexpr int NT = sk_chunk_tiles<D>(HG);
   decode_streamk_kernel<D, NT, BS, HG, kSkWaves><<<a.num_wg, 64 * kSkWaves, 0, s>>>(a);
-  const int pairs = a.num_seqs * (a.hkv / HG);
-  if (pairs > 0) merge_streamk_kernel<D, HG><<<pairs, 1024, 0, s>>>(a);
   return hipGetLastError();
 }
 

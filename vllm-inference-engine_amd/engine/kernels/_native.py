@@ -17,7 +17,7 @@ import torch  # noqa: F401  (must be loaded before the HIP library, see above)
 
 LIB_NAME = "libpa_gfx950.so"
 LIB_PATH = Path(__file__).with_name(LIB_NAME)
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 PA_OK = 0
 PA_ERR_ARG = 1
@@ -117,21 +117,30 @@ def stream_handle(device: torch.device) -> int:
 
 _workspaces: dict[tuple, torch.Tensor] = {}
 
+# Workspace kinds. "decode" serves pa_decode_batched_f16 and pa_decode_v2_f16:
+# its first bytes are the stream-K pair counters, which must be zero when a
+# buffer is first used and which every call leaves zero, so the buffer is
+# zero-filled on allocation and never lent to anything else. "scores" serves
+# pa_decode_v1_f16 (score rows, no zero requirement).
+WS_DECODE = "decode"
+WS_SCORES = "scores"
 
-def workspace(nbytes: int, device: torch.device, stream: int) -> int | None:
-    """Device address of a scratch buffer of at least nbytes for this (device, stream).
+
+def workspace(nbytes: int, device: torch.device, stream: int, kind: str = WS_DECODE) -> int | None:
+    """Device address of a scratch buffer of at least nbytes for this (device, stream, kind).
 
     The buffer is kept and reused by later calls on the same stream; work on
     one stream is ordered, so a call never overwrites scratch a previous call
     on that stream still reads. Calls on different streams get different
-    buffers. Memory comes from torch's caching allocator.
+    buffers. Memory comes from torch's caching allocator; a new buffer starts
+    zero-filled (the decode kernels' counters rely on it).
     """
     if nbytes == 0:
         return None
-    key = (device.index, stream)
+    key = (device.index, stream, kind)
     buf = _workspaces.get(key)
     if buf is None or buf.numel() < nbytes:
-        buf = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        buf = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
         _workspaces[key] = buf
     return buf.data_ptr()
 

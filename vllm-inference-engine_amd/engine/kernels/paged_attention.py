@@ -117,7 +117,8 @@ def paged_attention_decode_batched(
             seq_lens.data_ptr(),
             out.data_ptr(), _native.strides_of(out),
             num_seqs, num_q_heads, num_kv_heads, head_dim, block_size, num_blocks, max_blocks,
-            float(scale), _native.workspace(ws_bytes, dev, stream), ws_bytes, stream)
+            float(scale), _native.workspace(ws_bytes, dev, stream, _native.WS_DECODE), ws_bytes,
+            stream)
     _native.check(status, "pa_decode_batched_f16")
     return out
 
@@ -142,7 +143,8 @@ def _single_seq_args(q, k_cache, v_cache, block_table, seq_len):
     return num_q_heads, head_dim, num_blocks, block_size, num_kv_heads
 
 
-def _single_seq_call(fn_name, ws_name, q, k_cache, v_cache, block_table, seq_len, scale, ws_last):
+def _single_seq_call(fn_name, ws_name, q, k_cache, v_cache, block_table, seq_len, scale, ws_last,
+                     ws_kind):
     seq_len = int(seq_len)
     num_q_heads, head_dim, num_blocks, block_size, num_kv_heads = _single_seq_args(
         q, k_cache, v_cache, block_table, seq_len)
@@ -165,7 +167,7 @@ def _single_seq_call(fn_name, ws_name, q, k_cache, v_cache, block_table, seq_len
             block_table.data_ptr(), int(block_table.stride(0)), table_len, seq_len,
             out.data_ptr(), _native.strides_of(out),
             num_q_heads, num_kv_heads, head_dim, block_size, num_blocks, float(scale),
-            _native.workspace(ws_bytes, dev, stream), ws_bytes, stream)
+            _native.workspace(ws_bytes, dev, stream, ws_kind), ws_bytes, stream)
     _native.check(status, fn_name)
     return out
 
@@ -186,7 +188,7 @@ def paged_attention_decode_v1(
     """
     return _single_seq_call("pa_decode_v1_f16", "pa_decode_v1_workspace_bytes",
                             q, k_cache, v_cache, block_table, seq_len, scale,
-                            lambda table_len, n: n)
+                            lambda table_len, n: n, _native.WS_SCORES)
 
 
 def paged_attention_decode_v2(
@@ -200,7 +202,7 @@ def paged_attention_decode_v2(
     """Single-sequence online-softmax decode attention (reference paged_attention.py:419-470)."""
     return _single_seq_call("pa_decode_v2_f16", "pa_decode_v2_workspace_bytes",
                             q, k_cache, v_cache, block_table, seq_len, scale,
-                            lambda table_len, n: table_len)
+                            lambda table_len, n: table_len, _native.WS_DECODE)
 
 
 def pad_block_tables(
