@@ -150,10 +150,11 @@ static hipError_t launch_streamk_with(DecodeArgs& a, int num_seqs, int head_dim,
   const int want = kSkWgPerCu * device_cus();
   a.num_seqs = num_seqs;
   a.num_wg = want < bound ? want : bound;
-  // A pair segment costs a workgroup about as long as streaming 160 KB of K/V
-  // (measured on MI355X: pipeline fill plus the merge across wavefronts).
+  // A pair segment costs a workgroup about as long as streaming 240 KB of K/V
+  // (measured on MI355X: pipeline fill plus the drain and merge across
+  // wavefronts, 6-8 us per segment at the long-context shape).
   const int tile_bytes = 64 * streamk_head_group(a.hkv, head_dim) * head_dim;
-  a.seg_cost = (160 << 10) / tile_bytes;
+  a.seg_cost = (240 << 10) / tile_bytes;
   a.cnt = (int*)ws;
   a.recs = (float*)((char*)ws + kSkCounterBytes);
   return launch_decode_streamk(a, head_dim, s);
