@@ -49,7 +49,7 @@ enum {
 };
 
 /* ABI revision of this header; bumps whenever a signature or a workspace
- * contract changes (2: zero-initialised decode workspace). */
+ * contract changes (2: zero-initialised decode workspace; 3: pa_rope_kv_write_f16). */
 PA_API int pa_abi_version(void);
 
 /* Message of the last failed call on this thread ("" after a success). */
@@ -158,6 +158,37 @@ PA_API int pa_prefill_copy_f16(const void* key, const int64_t key_strides[3],
                         const int32_t* block_ids, int num_block_ids, int num_tokens,
                         int num_kv_heads, int head_dim, int block_size, int num_blocks,
                         void* stream);
+
+/*
+ * Fused rotary embedding and K/V write of one decode step. Replaces
+ * transformers' apply_rotary_pos_emb on the new token's q and k (called by
+ * paged_decode_attention_forward, engine/kernels/paged_attention_integration.py:108-109)
+ * together with that function's K/V write loop (:148-161; single sequence :120-133).
+ * q [num_seqs, num_q_heads, head_dim], key/value [num_seqs, num_kv_heads, head_dim]
+ * (any element strides) and cos/sin [num_seqs, head_dim] (the per-sequence row
+ * of the model's rotary table) are fp16. Writes
+ *   q_out[b, h]        = rot(q[b, h])
+ *   k_cache at slot    = rot(key[b, h]),  v_cache at slot = value[b, h]
+ * where the slot of sequence b is block block_tables[b][(L-1) / block_size],
+ * row (L-1) % block_size with L = seq_lens[b] (or uniform_seq_len when seq_lens
+ * is NULL), and rot(x)[j] = x[j] cos[j] - x[j + D/2] sin[j],
+ * rot(x)[j + D/2] = x[j + D/2] cos[j + D/2] + x[j] sin[j + D/2], every product and
+ * sum rounded to fp16 as transformers computes it in fp16, so the results are
+ * bit-identical to its apply_rotary_pos_emb. Rows whose slot is missing (L <= 0,
+ * block outside the table or the pool) are not written.
+ */
+PA_API int pa_rope_kv_write_f16(const void* q, const int64_t q_strides[3], const void* key,
+                                const int64_t key_strides[3], const void* value,
+                                const int64_t value_strides[3], const void* cos,
+                                const int64_t cos_strides[2], const void* sin,
+                                const int64_t sin_strides[2], void* q_out,
+                                const int64_t q_out_strides[3], void* k_cache,
+                                const int64_t k_strides[4], void* v_cache,
+                                const int64_t v_strides[4], const int32_t* block_tables,
+                                const int64_t bt_strides[2], const int32_t* seq_lens,
+                                int uniform_seq_len, int num_seqs, int num_q_heads,
+                                int num_kv_heads, int head_dim, int block_size, int num_blocks,
+                                int max_blocks_per_seq, void* stream);
 
 #ifdef __cplusplus
 }

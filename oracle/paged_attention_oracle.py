@@ -13,6 +13,8 @@ file:line in the reference repository:
   kv_write_reference               engine/kernels/paged_attention_integration.py:148-161
   kv_write_scatter                 same semantics, vectorised (cross-check of the loop)
   prefill_copy_reference           engine/kernels/paged_attention_integration.py:278-326
+  rope_fp16                        transformers apply_rotary_pos_emb (rotate_half form), as the
+                                   reference calls it at paged_attention_integration.py:108-109
 
 Pinning (tests/test_oracle.py): the attention oracle is checked against closed
 forms that do not share its code -- contiguous scaled-dot-product attention via
@@ -28,7 +30,11 @@ a vectorised scatter) and by block-id-encoded patterns. pad_block_tables is
 pinned by its specification (int32, zero padded, at least one column). The
 prefill copy is pinned by the reference's own exact-content fixture
 (tests/test_paged_attention_prefix_cache.py:60-125, restated on the GPU in
-tests/test_gpu_prefill_copy.py) besides this restatement.
+tests/test_gpu_prefill_copy.py) besides this restatement. rope_fp16 is pinned
+bit for bit against transformers' own apply_rotary_pos_emb (5.15.0, the
+version the reference pins in requirements.txt:3) on CPU fp16 tensors, and
+by closed forms (position 0 is the identity; a quarter turn maps (x1, x2) to
+(-x2, x1)).
 """
 from __future__ import annotations
 
@@ -156,3 +162,18 @@ def prefill_copy_reference(k_src: torch.Tensor, v_src: torch.Tensor, k_cache: to
     idx = torch.tensor(list(block_ids), dtype=torch.long)
     k_cache.index_copy_(0, idx, ks.reshape(nb, bs, *ks.shape[1:]).to(k_cache.dtype))
     v_cache.index_copy_(0, idx, vs.reshape(nb, bs, *vs.shape[1:]).to(v_cache.dtype))
+
+
+def rope_fp16(x: np.ndarray, cos: np.ndarray, sin: np.ndarray) -> np.ndarray:
+    """Rotary embedding of fp16 rows as transformers computes it in fp16.
+
+    x [..., D] with cos/sin broadcastable to it, all numpy float16. transformers'
+    apply_rotary_pos_emb (the reference's RoPE, paged_attention_integration.py:108-109)
+    evaluates (x * cos) + (rotate_half(x) * sin) with rotate_half(x) =
+    cat(-x[..., D/2:], x[..., :D/2]), each op rounded to fp16; numpy's float16
+    arithmetic rounds each op the same way.
+    """
+    assert x.dtype == np.float16 and cos.dtype == np.float16 and sin.dtype == np.float16
+    half = x.shape[-1] // 2
+    rot = np.concatenate([-x[..., half:], x[..., :half]], axis=-1)
+    return (x * cos) + (rot * sin)

@@ -166,7 +166,7 @@ using namespace pa;
 
 extern "C" {
 
-int pa_abi_version(void) { return 2; }
+int pa_abi_version(void) { return 3; }
 
 const char* pa_last_error(void) { return g_error.c_str(); }
 
@@ -503,6 +503,93 @@ int pa_prefill_copy_f16(const void* key, const int64_t key_strides[3], const voi
                    a.vc_st % 8 == 0 && a.vc_sh % 8 == 0 && aligned(key, 16) &&
                    aligned(value, 16) && aligned(k_cache, 16) && aligned(v_cache, 16);
   return finish_launch(launch_prefill_copy(a, vec, (hipStream_t)stream));
+}
+
+
+int pa_rope_kv_write_f16(const void* q, const int64_t q_strides[3], const void* key,
+                         const int64_t key_strides[3], const void* value,
+                         const int64_t value_strides[3], const void* cos,
+                         const int64_t cos_strides[2], const void* sin,
+                         const int64_t sin_strides[2], void* q_out,
+                         const int64_t q_out_strides[3], void* k_cache,
+                         const int64_t k_strides[4], void* v_cache, const int64_t v_strides[4],
+                         const int32_t* block_tables, const int64_t bt_strides[2],
+                         const int32_t* seq_lens, int uniform_seq_len, int num_seqs,
+                         int num_q_heads, int num_kv_heads, int head_dim, int block_size,
+                         int num_blocks, int max_blocks_per_seq, void* stream) {
+  clear_error();
+  if (num_seqs < 0) {
+    set_error("num_seqs must be >= 0");
+    return PA_ERR_ARG;
+  }
+  if (num_seqs == 0) return PA_OK;
+  if (!q || !key || !value || !cos || !sin || !q_out || !k_cache || !v_cache || !q_strides ||
+      !key_strides || !value_strides || !cos_strides || !sin_strides || !q_out_strides ||
+      !k_strides || !v_strides || !block_tables || !bt_strides) {
+    set_error("null pointer argument");
+    return PA_ERR_ARG;
+  }
+  if (num_q_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 || head_dim % 2 || block_size <= 0 ||
+      num_blocks <= 0 || max_blocks_per_seq <= 0) {
+    set_error("heads, an even head_dim, block_size, num_blocks and the table width must be "
+              "positive");
+    return PA_ERR_ARG;
+  }
+  if (k_strides[3] != 1 || v_strides[3] != 1 || q_out_strides[2] != 1) {
+    set_error("cache and q_out head_dim stride must be 1");
+    return PA_ERR_ARG;
+  }
+  RopeKVArgs a{};
+  a.q = (const uint16_t*)q;
+  a.qs_b = q_strides[0];
+  a.qs_h = q_strides[1];
+  a.qs_d = q_strides[2];
+  a.key = (const uint16_t*)key;
+  a.ks_b = key_strides[0];
+  a.ks_h = key_strides[1];
+  a.ks_d = key_strides[2];
+  a.val = (const uint16_t*)value;
+  a.vs_b = value_strides[0];
+  a.vs_h = value_strides[1];
+  a.vs_d = value_strides[2];
+  a.cos = (const uint16_t*)cos;
+  a.cs_b = cos_strides[0];
+  a.cs_d = cos_strides[1];
+  a.sin = (const uint16_t*)sin;
+  a.ss_b = sin_strides[0];
+  a.ss_d = sin_strides[1];
+  a.q_out = (uint16_t*)q_out;
+  a.qo_b = q_out_strides[0];
+  a.qo_h = q_out_strides[1];
+  a.kc = (uint16_t*)k_cache;
+  a.kc_sb = k_strides[0];
+  a.kc_st = k_strides[1];
+  a.kc_sh = k_strides[2];
+  a.vc = (uint16_t*)v_cache;
+  a.vc_sb = v_strides[0];
+  a.vc_st = v_strides[1];
+  a.vc_sh = v_strides[2];
+  a.bt = block_tables;
+  a.bt_sb = bt_strides[0];
+  a.bt_sk = bt_strides[1];
+  a.lens = seq_lens;
+  a.uniform_len = uniform_seq_len;
+  a.num_seqs = num_seqs;
+  a.hq = num_q_heads;
+  a.hkv = num_kv_heads;
+  a.D = head_dim;
+  a.bs = block_size;
+  a.num_blocks = num_blocks;
+  a.max_blocks = max_blocks_per_seq;
+  auto rows16 = [](const void* p, int64_t sb, int64_t sh, int64_t sd) {
+    return aligned(p, 16) && sd == 1 && sb % 8 == 0 && sh % 8 == 0;
+  };
+  const bool vec = head_dim % 16 == 0 && rows16(q, a.qs_b, a.qs_h, a.qs_d) &&
+                   rows16(key, a.ks_b, a.ks_h, a.ks_d) && rows16(value, a.vs_b, a.vs_h, a.vs_d) &&
+                   rows16(cos, a.cs_b, 0, a.cs_d) && rows16(sin, a.ss_b, 0, a.ss_d) &&
+                   rows16(q_out, a.qo_b, a.qo_h, 1) && rows16(k_cache, a.kc_sb, a.kc_st, 1) &&
+                   a.kc_sh % 8 == 0 && rows16(v_cache, a.vc_sb, a.vc_st, 1) && a.vc_sh % 8 == 0;
+  return finish_launch(launch_rope_kv_write(a, vec, (hipStream_t)stream));
 }
 
 }  // extern "C"

@@ -93,11 +93,40 @@ struct PrefillCopyArgs {
   int num_ids, num_tokens, hkv, D, bs, num_blocks;
 };
 
+// Argument bundle of the fused rotary embedding + K/V write: q, key and value
+// rows [num_seqs, heads, D] with any element strides, per-sequence cos/sin
+// rows [num_seqs, D]; rotated queries go to q_out, rotated keys and values to
+// the new token's cache slot.
+struct RopeKVArgs {
+  const uint16_t* q;
+  int64_t qs_b, qs_h, qs_d;
+  const uint16_t* key;
+  int64_t ks_b, ks_h, ks_d;
+  const uint16_t* val;
+  int64_t vs_b, vs_h, vs_d;
+  const uint16_t* cos;
+  int64_t cs_b, cs_d;
+  const uint16_t* sin;
+  int64_t ss_b, ss_d;
+  uint16_t* q_out;
+  int64_t qo_b, qo_h;
+  uint16_t* kc;
+  int64_t kc_sb, kc_st, kc_sh;
+  uint16_t* vc;
+  int64_t vc_sb, vc_st, vc_sh;
+  const int32_t* bt;
+  int64_t bt_sb, bt_sk;
+  const int32_t* lens;  // per-sequence lengths, or null: use uniform_len
+  int uniform_len;
+  int num_seqs, hq, hkv, D, bs, num_blocks, max_blocks;
+};
+
 // Launchers (defined next to their kernels).
 hipError_t launch_decode_split(const DecodeArgs& a, int D, int num_seqs, hipStream_t s);
 hipError_t launch_decode_v1(const DecodeArgs& a, int D, hipStream_t s);
 hipError_t launch_kv_write(const KVWriteArgs& a, bool vec, hipStream_t s);
 hipError_t launch_prefill_copy(const PrefillCopyArgs& a, bool vec, hipStream_t s);
+hipError_t launch_rope_kv_write(const RopeKVArgs& a, bool vec, hipStream_t s);
 hipError_t launch_decode_streamk(const DecodeArgs& a, int D, hipStream_t s);
 int streamk_head_group(int num_kv_heads, int D);
 

@@ -17,7 +17,7 @@ import torch  # noqa: F401  (must be loaded before the HIP library, see above)
 
 LIB_NAME = "libpa_gfx950.so"
 LIB_PATH = Path(__file__).with_name(LIB_NAME)
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 PA_OK = 0
 PA_ERR_ARG = 1
@@ -54,6 +54,10 @@ SIGNATURES: dict[str, tuple] = {
     "pa_prefill_copy_f16": (_i32, [
         _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i32, _i32,
         _i32, _i32, _i32, _i32, _vp]),
+    "pa_rope_kv_write_f16": (_i32, [
+        _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p,
+        _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i32,
+        _i32, _i32, _i32, _i32, _i32, _i32, _i32, _vp]),
 }
 
 _lib = None

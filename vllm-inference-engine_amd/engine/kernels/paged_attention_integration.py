@@ -24,6 +24,7 @@ import math
 from contextlib import contextmanager
 from typing import Any, Callable, List, Optional, Tuple, Union
 
+import numpy as np
 import torch
 import torch.nn as nn
 
@@ -33,6 +34,7 @@ from .paged_attention import _on_device, pad_block_tables, paged_attention_decod
 __all__ = [
     "PagedAttentionContext",
     "paged_kv_write",
+    "paged_rope_kv_write",
     "paged_prefill_copy",
     "paged_decode_attention_forward",
     "patch_paged_attention",
@@ -103,6 +105,81 @@ def paged_kv_write(
     _native.check(status, "pa_kv_write_f16")
 
 
+def _rope_rows(t: torch.Tensor) -> torch.Tensor:
+    """cos/sin as one row per sequence: [B, 1, D] (the model's rotary output) or [B, D]."""
+    if t.dim() == 3:
+        assert t.shape[1] == 1, f"expected one position per sequence, got shape {tuple(t.shape)}"
+        t = t.squeeze(1)
+    assert t.dim() == 2, f"expected [num_seqs, head_dim], got {tuple(t.shape)}"
+    return t
+
+
+def paged_rope_kv_write(
+    query: torch.Tensor,         # [num_seqs, num_q_heads, (1,) head_dim] fp16, any strides
+    key: torch.Tensor,           # [num_seqs, num_kv_heads, (1,) head_dim]
+    value: torch.Tensor,         # same as key
+    cos: torch.Tensor,           # [num_seqs, (1,) head_dim] fp16, the rotary table rows
+    sin: torch.Tensor,
+    k_cache: torch.Tensor,       # [num_blocks, block_size, num_kv_heads, head_dim] fp16
+    v_cache: torch.Tensor,
+    block_tables: torch.Tensor,  # [num_seqs, max_blocks_per_seq] int32 (or 1-D for one sequence)
+    seq_lens: Union[torch.Tensor, int],
+) -> torch.Tensor:
+    """Rotary embedding of the new token's q and k plus its K/V write, in one launch.
+
+    Same results, bit for bit, as transformers' apply_rotary_pos_emb in fp16
+    (called by the reference at integration.py:108-109) followed by
+    paged_kv_write of the rotated key and the value (reference write loop
+    :148-161): returns the rotated queries [num_seqs, num_q_heads, head_dim]
+    (contiguous) and writes the rotated key and the value into each sequence's
+    slot of position L_b - 1. Asynchronous; no host synchronisation.
+    """
+    query = _as_rows(query)
+    key = _as_rows(key)
+    value = _as_rows(value)
+    cos = _rope_rows(cos)
+    sin = _rope_rows(sin)
+    for t in (query, key, value, cos, sin, k_cache, v_cache):
+        assert t.is_cuda and t.dtype == torch.float16
+    assert block_tables.dtype == torch.int32 and block_tables.is_cuda
+    assert k_cache.shape == v_cache.shape, "k_cache and v_cache must have the same shape"
+    num_blocks, block_size, num_kv_heads, head_dim = k_cache.shape
+    num_seqs, num_q_heads = query.shape[0], query.shape[1]
+    assert query.shape[2] == head_dim and head_dim % 2 == 0
+    assert key.shape == (num_seqs, num_kv_heads, head_dim) and value.shape == key.shape
+    assert cos.shape == (num_seqs, head_dim) and sin.shape == cos.shape
+    if block_tables.dim() == 1:
+        block_tables = block_tables.unsqueeze(0)
+    assert block_tables.shape[0] == num_seqs
+    if isinstance(seq_lens, torch.Tensor):
+        assert seq_lens.is_cuda and seq_lens.dtype == torch.int32 and seq_lens.shape == (num_seqs,)
+        lens_ptr, uniform = _native.ptr(seq_lens), 0
+    else:
+        assert num_seqs == 1, "a host integer length is only accepted for one sequence"
+        lens_ptr, uniform = None, int(seq_lens)
+    q_out = torch.empty((num_seqs, num_q_heads, head_dim), dtype=torch.float16, device=query.device)
+    if num_seqs == 0:
+        return q_out
+    lib = _native.load()
+    dev = query.device
+    with _on_device(dev):
+        status = lib.pa_rope_kv_write_f16(
+            query.data_ptr(), _native.strides_of(query),
+            key.data_ptr(), _native.strides_of(key),
+            value.data_ptr(), _native.strides_of(value),
+            cos.data_ptr(), _native.strides_of(cos),
+            sin.data_ptr(), _native.strides_of(sin),
+            q_out.data_ptr(), _native.strides_of(q_out),
+            k_cache.data_ptr(), _native.strides_of(k_cache),
+            v_cache.data_ptr(), _native.strides_of(v_cache),
+            block_tables.data_ptr(), _native.strides_of(block_tables),
+            lens_ptr, uniform,
+            num_seqs, num_q_heads, num_kv_heads, head_dim, block_size, num_blocks,
+            block_tables.shape[1], _native.stream_handle(dev))
+    _native.check(status, "pa_rope_kv_write_f16")
+    return q_out
+
+
 class PagedAttentionContext:
     """Per-step metadata handed to the patched attention modules (reference integration.py:29-62).
 
@@ -138,6 +215,20 @@ class PagedAttentionContext:
             else:
                 self.seq_lens_tensor = torch.tensor(seq_lens, dtype=torch.int32, device=pool.device)
 
+    @classmethod
+    def from_device(cls, pool: Any, block_tables: torch.Tensor, seq_lens: torch.Tensor,
+                    block_size: int = 16) -> "PagedAttentionContext":
+        """Batched context over tables and lengths already on the device (no host copies)."""
+        ctx = cls.__new__(cls)
+        ctx.pool = pool
+        ctx.block_size = block_size
+        ctx.is_decode = True
+        ctx.is_batched = True
+        ctx.block_table_list = None
+        ctx.padded_block_tables = block_tables
+        ctx.seq_lens_tensor = seq_lens
+        return ctx
+
 
 def paged_decode_attention_forward(
     self: nn.Module,
@@ -149,9 +240,11 @@ def paged_decode_attention_forward(
 ) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
     """Drop-in Qwen2Attention.forward for one decode step (reference integration.py:65-176).
 
-    q/k/v projections, RoPE, the new K/V written into the pool with one
-    paged_kv_write launch, batched paged attention over L_b tokens (the write
-    precedes the read, as in the reference), then o_proj.
+    q/k/v projections; RoPE of q and k together with the new K/V's write into
+    the pool in one paged_rope_kv_write launch (bit-identical to transformers'
+    apply_rotary_pos_emb followed by the reference's write loop); batched paged
+    attention over L_b tokens (the write precedes the read, as in the
+    reference); then o_proj.
     """
     ctx: Optional[PagedAttentionContext] = getattr(self, "_paged_attention_context", None)
     if ctx is None or not ctx.is_decode:
@@ -166,8 +259,6 @@ def paged_decode_attention_forward(
             )
         raise RuntimeError("No fallback forward method found on attention module.")
 
-    from transformers.models.qwen2.modeling_qwen2 import apply_rotary_pos_emb
-
     layer_idx = self.layer_idx
     input_shape = hidden_states.shape[:-1]  # [batch, 1]
     hidden_shape = (*input_shape, -1, self.head_dim)
@@ -177,7 +268,6 @@ def paged_decode_attention_forward(
     value_states = self.v_proj(hidden_states).view(hidden_shape).transpose(1, 2)
 
     cos, sin = position_embeddings
-    query_states, key_states = apply_rotary_pos_emb(query_states, key_states, cos, sin)
 
     scale = self.scaling if hasattr(self, "scaling") else 1.0 / math.sqrt(self.head_dim)
     pool = ctx.pool
@@ -187,16 +277,18 @@ def paged_decode_attention_forward(
     if not ctx.is_batched:
         bt = ctx.block_table_tensor
         seq_len = ctx.single_seq_len
-        paged_kv_write(key_states, value_states, k_cache, v_cache, bt, seq_len)
+        q_rot = paged_rope_kv_write(query_states, key_states, value_states, cos, sin,
+                                    k_cache, v_cache, bt, seq_len)
         seq_lens_t = torch.tensor([seq_len], dtype=torch.int32, device=pool.device)
         bt_2d = bt.unsqueeze(0)
     else:
         bt_2d = ctx.padded_block_tables
         seq_lens_t = ctx.seq_lens_tensor
-        paged_kv_write(key_states, value_states, k_cache, v_cache, bt_2d, seq_lens_t)
+        q_rot = paged_rope_kv_write(query_states, key_states, value_states, cos, sin,
+                                    k_cache, v_cache, bt_2d, seq_lens_t)
 
     attn_output = paged_attention_decode_batched(
-        q=query_states.squeeze(2),
+        q=q_rot,
         k_cache=k_cache,
         v_cache=v_cache,
         block_tables=bt_2d,
@@ -268,6 +360,80 @@ def paged_prefill_copy(
     _native.check(status, "pa_prefill_copy_f16")
 
 
+class _DecodeGraph:
+    """One decode step captured as a HIP graph for a fixed batch size and table width.
+
+    Static device buffers hold the step's inputs: token ids and lengths (one
+    pinned host-to-device copy per step, unpacked inside the graph) and the
+    zero-padded block tables (copied only when a row changed: a sequence
+    gained a block or the batch was reordered). The graph replays the whole
+    model forward -- each layer's fused RoPE + K/V write and paged attention
+    included -- so a step costs one replay instead of a few hundred kernel
+    launches from Python. The greedy token and top-1/top-2 margin are computed
+    after the replay, outside the graph: top-k and arg-max over a full
+    vocabulary row use multi-block reductions whose scratch is cleared with
+    memset operations, which are not captured into the graph. The capture runs
+    on the graph's own stream, so the decode workspace its kernels use is its
+    own.
+    """
+
+    def __init__(self, runner: "KernelPagedManualDecode", batch: int, width: int):
+        dev = runner.device
+        self.batch, self.width = batch, width
+        self.stream = torch.cuda.Stream(dev)
+        self.host_in = torch.zeros(2, batch, dtype=torch.long).pin_memory()  # ids, lengths
+        self.dev_in = torch.zeros(2, batch, dtype=torch.long, device=dev)
+        self.host_tables = torch.zeros(batch, width, dtype=torch.int32).pin_memory()
+        self.tables = torch.zeros(batch, width, dtype=torch.int32, device=dev)
+        self.mirror = np.full((batch, width), -1, dtype=np.int32)  # table contents on the device
+        self.ids = torch.zeros(batch, 1, dtype=torch.long, device=dev)
+        self.pos = torch.zeros(batch, 1, dtype=torch.long, device=dev)
+        self.lens = torch.ones(batch, dtype=torch.int32, device=dev)
+        self.ctx = PagedAttentionContext.from_device(runner.pool, self.tables, self.lens,
+                                                     runner.block_size)
+        self.runner = runner
+        self.graph: Optional[torch.cuda.CUDAGraph] = None
+        self.logits: Optional[torch.Tensor] = None
+
+    def _body(self):
+        self.ids.copy_(self.dev_in[0].view(-1, 1))
+        self.lens.copy_(self.dev_in[1])
+        self.pos.copy_((self.dev_in[1] - 1).view(-1, 1))
+        model = self.runner.model
+        with patch_paged_attention(model, self.ctx):
+            out = model(input_ids=self.ids, position_ids=self.pos, use_cache=False)
+        return out.logits[:, -1, :]
+
+    def load(self, tokens: List[int], lens: List[int], rows: List[List[int]]) -> None:
+        """Stage this step's inputs (asynchronous copies on the current stream)."""
+        hin = self.host_in.numpy()
+        hin[0] = tokens
+        hin[1] = lens
+        self.dev_in.copy_(self.host_in, non_blocking=True)
+        table = np.zeros((self.batch, self.width), dtype=np.int32)
+        for i, r in enumerate(rows):
+            table[i, :len(r)] = r
+        if not np.array_equal(table, self.mirror):
+            self.host_tables.numpy()[:] = table
+            self.tables.copy_(self.host_tables, non_blocking=True)
+            self.mirror = table
+
+    def run(self) -> torch.Tensor:
+        """Replays the step (capturing it on first use); returns the last-position logits."""
+        if self.graph is None:
+            cur = torch.cuda.current_stream(self.runner.device)
+            self.stream.wait_stream(cur)
+            with torch.cuda.stream(self.stream):
+                for _ in range(2):  # warm-up: libraries pick kernels, scratch is allocated
+                    self._body()
+            cur.wait_stream(self.stream)
+            self.graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(self.graph, stream=self.stream):
+                self.logits = self._body()
+        self.graph.replay()
+        return self.logits
+
+
 def _seq_field(seq, name, default=None):
     if isinstance(seq, dict):
         return seq.get(name, default)
@@ -288,10 +454,13 @@ class KernelPagedManualDecode:
     blocks are written into the pool with paged_prefill_copy (prefix modes
     "off", "share", "full" as in the reference). decode_step(seqs): one
     batched forward with paged_decode_attention_forward patched into every
-    attention module, so each layer runs paged_kv_write + the batched paged
-    attention kernel. The step makes one device-to-host transfer (tokens and
-    top-1/top-2 margins together) instead of the reference's per-sequence
-    logits copies (:643-651); `last_logits` stays on the device.
+    attention module, so each layer runs the fused RoPE + K/V write and the
+    batched paged attention kernel. With use_graphs (the default) the forward
+    is captured once per (batch size, table width) as a HIP graph over
+    persistent device tables and lengths, and each step replays it. The step
+    makes one device-to-host transfer (tokens and top-1/top-2 margins
+    together) instead of the reference's per-sequence logits copies
+    (:643-651); `last_logits` stays on the device.
     """
 
     def __init__(
@@ -305,6 +474,7 @@ class KernelPagedManualDecode:
         dtype: torch.dtype = torch.float16,
         debug_prefix_cache: bool = False,
         prefix_mode: str = "off",
+        use_graphs: bool = True,
     ):
         from ..memory.block_pool import FreeListAllocator, PhysicalBlockPool
 
@@ -333,6 +503,10 @@ class KernelPagedManualDecode:
                                       head_dim=self.head_dim, dtype=dtype, device=self.device)
         self.allocator = FreeListAllocator(num_blocks)
         self._grad_probed = False
+        # Batched decode steps replay captured HIP graphs, one per (batch size,
+        # table width rounded up to a multiple of 64 blocks).
+        self.use_graphs = use_graphs
+        self._graphs: dict = {}
 
     # -- prefill -----------------------------------------------------------------
     def _copy_prefill_kv(self, pkv: Any, block_table: Any, prompt_len: int, skip_blocks: int = 0) -> None:
@@ -450,15 +624,25 @@ class KernelPagedManualDecode:
                     raise ValueError("Sequence must provide last_token_id or non-empty generated_ids.")
                 last = gen[-1]
             last_tokens.append(int(last))
-        input_ids = torch.tensor(last_tokens, dtype=torch.long, device=self.device).unsqueeze(1)
-        position_ids = torch.tensor([[L - 1] for L in seq_lens], dtype=torch.long, device=self.device)
-        ctx = PagedAttentionContext(self.pool, tables, seq_lens, self.block_size, True)
-        with patch_paged_attention(self.model, ctx):
-            out = self.model(input_ids=input_ids, position_ids=position_ids, use_cache=False)
-        logits = out.logits[:, -1, :]
+        if self.use_graphs:
+            rows = [list(bt.physical_block_ids) for bt in tables]
+            width = max(64, -(-max(len(r) for r in rows) // 64) * 64)
+            graph = self._graphs.get((n, width))
+            if graph is None:
+                graph = self._graphs[(n, width)] = _DecodeGraph(self, n, width)
+            graph.load(last_tokens, seq_lens, rows)
+            logits = graph.run().clone()  # the graph's output buffer is reused by the next step
+        else:
+            input_ids = torch.tensor(last_tokens, dtype=torch.long, device=self.device).unsqueeze(1)
+            position_ids = torch.tensor([[L - 1] for L in seq_lens], dtype=torch.long,
+                                        device=self.device)
+            ctx = PagedAttentionContext(self.pool, tables, seq_lens, self.block_size, True)
+            with patch_paged_attention(self.model, ctx):
+                out = self.model(input_ids=input_ids, position_ids=position_ids, use_cache=False)
+            logits = out.logits[:, -1, :]
         top2 = torch.topk(logits, k=2, dim=-1).values.double()
-        # float64 holds every token id exactly: tokens and margins in one transfer.
         both = torch.stack([torch.argmax(logits, dim=-1).double(), top2[:, 0] - top2[:, 1]])
+        # float64 holds every token id exactly: tokens and margins in one transfer.
         toks, margins = both.tolist()
         for i, seq in enumerate(seqs):
             _set_seq_field(seq, "last_logits", logits[i].detach())
