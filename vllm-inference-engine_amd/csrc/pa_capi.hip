@@ -128,6 +128,9 @@ static bool streamk_ok(int num_seqs, int num_kv_heads, int head_dim) {
   return num_seqs <= kSkMaxSeqs && (int64_t)(num_kv_heads / hg) * num_seqs <= kSkMaxPairs;
 }
 
+// Longest pair (in 16-token tiles) that the one-workgroup-per-pair schedule takes.
+constexpr int kPairTilesMax = 128;
+
 // Compute units of the current device (cached per device).
 static int device_cus() {
   static int cache[64] = {0};
@@ -150,6 +153,12 @@ static hipError_t launch_streamk_with(DecodeArgs& a, int num_seqs, int head_dim,
   const int want = kSkWgPerCu * device_cus();
   a.num_seqs = num_seqs;
   a.num_wg = want < bound ? want : bound;
+  // Pairs no longer than kPairTilesMax tiles (bounded by the table width) that
+  // all fit the GPU at once run one per workgroup: splitting them would cost
+  // more in segment starts and merges than it balances.
+  const int pairs = num_seqs * (a.hkv / streamk_head_group(a.hkv, head_dim));
+  a.pair_per_wg = pairs <= want && max_tiles_for(a.max_blocks, a.bs) <= kPairTilesMax;
+  if (a.pair_per_wg) a.num_wg = pairs;
   // A pair segment costs a workgroup about as long as streaming 240 KB of K/V
   // (measured on MI355X: pipeline fill plus the drain and merge across
   // wavefronts, 6-8 us per segment at the long-context shape).

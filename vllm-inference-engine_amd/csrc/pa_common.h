@@ -48,6 +48,9 @@ struct DecodeArgs {
   // Fixed cost of a pair segment (pipeline fill, cross-wavefront merge),
   // in tiles: the schedule splits tiles plus this cost per pair evenly.
   int seg_cost;
+  // Nonzero: one workgroup per (sequence, kv-head group) pair instead of
+  // equal ranges of the pair list (small batches of short sequences).
+  int pair_per_wg;
 };
 
 // Stream-K limits: sequences whose tile prefix fits the LDS plan, the largest

@@ -8,12 +8,14 @@
 // workgroup derives the plan itself: its threads load the lengths, scan the
 // per-sequence tile counts into LDS and binary-search their range's first pair.
 //
-// Within a range the workgroup walks pair segments. The eight wavefronts
-// claim the segment's chunks (NT tiles) from an LDS counter, each keeping an
-// online softmax per query head, and merge their states through LDS at the
-// end of the segment. A pair wholly inside the range is written as final fp16 output; a
-// pair cut by a range boundary leaves an fp32 partial record (at most two per
-// workgroup) that merge_streamk_kernel combines by log-sum-exp.
+// Within a range the workgroup walks pair segments. Wavefront w takes chunks
+// (NT tiles) w, w + 8, w + 16, ... of the segment, keeping an online softmax
+// per query head, and the eight wavefronts merge their states through LDS in
+// a fixed order at the end of the segment, so results are the same bits on
+// every run. A pair wholly inside the range is written as final fp16 output;
+// a pair cut by a range boundary leaves an fp32 partial record (at most two
+// per workgroup), and the last workgroup to finish such a pair combines its
+// records by log-sum-exp, in record order.
 //
 // Per tile a wavefront loads the K and V rows of HG adjacent kv heads with
 // whole-cache-line, non-temporal 16-byte loads (whole contiguous token rows
@@ -114,7 +116,6 @@ void decode_streamk_kernel(DecodeArgs a) {
   __shared__ __attribute__((aligned(16))) char smem[NW * WAVE_BYTES];
   __shared__ int s_pref[kSkMaxSeqs + 1];
   __shared__ int s_wtot[NW];
-  __shared__ int s_next;  // next unclaimed chunk of the current segment
   __shared__ int s_merge[2];  // pairs this workgroup completes (-1: none)
 
   const int tid = threadIdx.x;
@@ -169,10 +170,7 @@ void decode_streamk_kernel(DecodeArgs a) {
       if (b < B) s_pref[b] = run;
       run += cnt[i];
     }
-    if (tid == 0) {
-      s_pref[B] = total;
-      s_next = 0;
-    }
+    if (tid == 0) s_pref[B] = total;
     __syncthreads();
   }
 
@@ -190,9 +188,21 @@ void decode_streamk_kernel(DecodeArgs a) {
   // Workgroups beyond the tile count get no range, so every range is non-empty.
   const int64_t T = (int64_t)NHG * s_pref[B];
   const int Ge = (int)(T < G ? T : G);
-  if (wg >= Ge) return;
-  const int64_t x0 = range_start(wg, T, Ge);
-  const int64_t x1 = range_start(wg + 1, T, Ge);
+  int64_t x0, x1;
+  if (a.pair_per_wg) {
+    // Small batches of short pairs: workgroup w takes pair w whole, so no pair
+    // is cut, no partial record is written and no merge is needed.
+    if (wg >= B * NHG) return;
+    const int pb = wg / NHG;
+    const int width = s_pref[pb + 1] - s_pref[pb];
+    if (width == 0) return;  // a zero-length sequence: its rows were written above
+    x0 = (int64_t)NHG * s_pref[pb] + (int64_t)(wg - pb * NHG) * width;
+    x1 = x0 + width;
+  } else {
+    if (wg >= Ge) return;
+    x0 = range_start(wg, T, Ge);
+    x1 = range_start(wg + 1, T, Ge);
+  }
 
   // First pair: the last sequence whose pairs start at or before x0.
   int b;
@@ -462,11 +472,11 @@ void decode_streamk_kernel(DecodeArgs a) {
         wave_lds_fence();
       };
 
-      // Wavefront-local pipeline over the chunks this wavefront claims. The
-      // wavefronts of the workgroup claim the segment's chunks one at a time
-      // from an LDS counter, so a wavefront that runs faster (the hardware
-      // favours older wavefronts) takes more of them and all finish together.
-      // Step s computes chunk c_s: K/V register sets Y0/Y1 hold steps s and
+      // Wavefront-local pipeline over this wavefront's chunks: wavefront w
+      // takes chunks w, w + NW, w + 2 NW, ... A fixed assignment (rather than
+      // claims from a shared counter, which let faster wavefronts take more
+      // chunks) keeps the summation order, and so the result bits, the same
+      // on every run; it costs about 1% at large batches. Step s computes chunk c_s: K/V register sets Y0/Y1 hold steps s and
       // s+1, id sets X0/X1 the block ids of steps s+2 and s+3. At step s: stage
       // Y[s%2] into LDS, reuse it for the loads of step s+2 (ids in X[s%2]),
       // claim step s+3 and fetch its ids into X[(s+1)%2], then compute step s.
@@ -474,10 +484,11 @@ void decode_streamk_kernel(DecodeArgs a) {
       // ends its work; loads of such chunks are issued anyway (empty resources,
       // clamped table reads) so that no branch separates them.
       const int nck = __builtin_amdgcn_readfirstlane((s1 - s0 + NT - 1) / NT);
+      int next_chunk = wave;
       auto claim = [&]() {
-        int c = 0;
-        if (lane == 0) c = __hip_atomic_fetch_add(&s_next, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-        return __builtin_amdgcn_readfirstlane(c);
+        const int c = next_chunk;
+        next_chunk += NW;
+        return c;
       };
       {
         u32x4 kb0[NT][NI], vb0[NT][NI], kb1[NT][NI], vb1[NT][NI];
@@ -521,8 +532,7 @@ void decode_streamk_kernel(DecodeArgs a) {
       // lane, so the 16-byte LDS writes are conflict-free). Wavefront w then
       // combines chunks j = w, w + NW, ... of all wavefronts and stores them.
       float* cm = reinterpret_cast<float*>(my_smem);
-      __syncthreads();  // every wavefront is done with its staging buffers and its claims
-      if (tid == 0) s_next = 0;  // published to the next segment by the barriers below
+      __syncthreads();  // every wavefront is done with its staging buffers
 #pragma unroll
       for (int hg = 0; hg < HG; ++hg) {
         float l = l_run[hg];
