@@ -49,7 +49,8 @@ enum {
 };
 
 /* ABI revision of this header; bumps whenever a signature or a workspace
- * contract changes (2: zero-initialised decode workspace; 3: pa_rope_kv_write_f16). */
+ * contract changes (2: zero-initialised decode workspace; 3: pa_rope_kv_write_f16;
+ * 4: pa_prefill_attention_f16). */
 PA_API int pa_abi_version(void);
 
 /* Message of the last failed call on this thread ("" after a success). */
@@ -189,6 +190,36 @@ PA_API int pa_rope_kv_write_f16(const void* q, const int64_t q_strides[3], const
                                 int uniform_seq_len, int num_seqs, int num_q_heads,
                                 int num_kv_heads, int head_dim, int block_size, int num_blocks,
                                 int max_blocks_per_seq, void* stream);
+
+/*
+ * Paged prefill attention: the new tokens of each sequence attend causally over
+ * the sequence's pool rows. Replaces the "full" prefix-cache prefill's
+ * attention (engine/kernels/paged_attention_integration.py:459-482: the cached
+ * prefix blocks gathered into a DynamicCache, :364-392, and the prompt suffix
+ * forwarded through transformers' attention with a causal mask), reading the
+ * prefix from the pool where it lies instead of copying it out.
+ *   q     [num_tokens, num_q_heads, head_dim]; sequence b owns rows
+ *         query_start_loc[b] .. query_start_loc[b + 1] - 1 (n_b rows; int32
+ *         device array of num_seqs + 1 non-decreasing entries)
+ *   seq_lens[b] = context length L_b after the new tokens; their K/V must
+ *         already be in the pool at positions L_b - n_b .. L_b - 1
+ *   out   [num_tokens, num_q_heads, head_dim]
+ * Row i of sequence b (position p = L_b - n_b + i) gets
+ * softmax(scale * q k^T) v over pool positions 0 .. p, query head h reading kv
+ * head h / (num_q_heads / num_kv_heads). max_query_len must be at least every
+ * n_b (rows past it are not computed); rows with p < 0 are written as zeros;
+ * rows outside every sequence's range are not written. Needs no workspace.
+ */
+PA_API int pa_prefill_attention_f16(const void* q, const int64_t q_strides[3],
+                                    const void* k_cache, const int64_t k_strides[4],
+                                    const void* v_cache, const int64_t v_strides[4],
+                                    const int32_t* block_tables, const int64_t bt_strides[2],
+                                    const int32_t* seq_lens, const int32_t* query_start_loc,
+                                    int max_query_len, void* out, const int64_t out_strides[3],
+                                    int num_seqs, int num_tokens, int num_q_heads,
+                                    int num_kv_heads, int head_dim, int block_size,
+                                    int num_blocks, int max_blocks_per_seq, float scale,
+                                    void* stream);
 
 #ifdef __cplusplus
 }

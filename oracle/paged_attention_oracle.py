@@ -15,6 +15,10 @@ file:line in the reference repository:
   prefill_copy_reference           engine/kernels/paged_attention_integration.py:278-326
   rope_fp16                        transformers apply_rotary_pos_emb (rotate_half form), as the
                                    reference calls it at paged_attention_integration.py:108-109
+  prefix_prefill_attention         "full" prefix-cache mode: the uncached prompt suffix
+                                   attends causally over the cached blocks plus itself
+                                   (engine/kernels/paged_attention_integration.py:459-482,
+                                   prefix gathered as :364-392)
 
 Pinning (tests/test_oracle.py): the attention oracle is checked against closed
 forms that do not share its code -- contiguous scaled-dot-product attention via
@@ -34,7 +38,14 @@ tests/test_gpu_prefill_copy.py) besides this restatement. rope_fp16 is pinned
 bit for bit against transformers' own apply_rotary_pos_emb (5.15.0, the
 version the reference pins in requirements.txt:3) on CPU fp16 tensors, and
 by closed forms (position 0 is the identity; a quarter turn maps (x1, x2) to
-(-x2, x1)).
+(-x2, x1)). prefix_prefill_attention is pinned (tests/test_oracle_prefill.py)
+against code it does not share: with one new token it equals
+naive_reference_paged_attention; its rows equal the last rows of
+torch's causal scaled_dot_product_attention (is_causal=True) over the whole
+gathered sequence, which fixes the position offset and the mask boundary; an
+fp64 brute force with explicit loops agrees on tiny sizes; and planted
+mistakes (mask off by one, positions counted from the suffix start, kv head
+h % Hkv) each fail one of these.
 """
 from __future__ import annotations
 
@@ -177,3 +188,55 @@ def rope_fp16(x: np.ndarray, cos: np.ndarray, sin: np.ndarray) -> np.ndarray:
     half = x.shape[-1] // 2
     rot = np.concatenate([-x[..., half:], x[..., :half]], axis=-1)
     return (x * cos) + (rot * sin)
+
+
+def prefix_prefill_attention(
+    q: torch.Tensor,              # [num_tokens, num_q_heads, head_dim], sequences packed in order
+    k_cache: torch.Tensor,        # [num_blocks, block_size, num_kv_heads, head_dim]
+    v_cache: torch.Tensor,
+    block_tables: Sequence[Sequence[int]],
+    seq_lens: Sequence[int],      # context length after the new tokens (cached + new)
+    query_lens: Sequence[int],    # new tokens per sequence; their rows are consecutive in q
+    scale: float,
+    compute_dtype: torch.dtype = torch.float32,
+) -> torch.Tensor:
+    """Causal attention of each sequence's new tokens over its whole paged context.
+
+    The reference's "full" prefix-cache mode (paged_attention_integration.py:459-482)
+    gathers the cached prefix blocks into a DynamicCache (:364-392) and forwards
+    only the prompt suffix with position_ids cached..prompt_len-1 and an all-ones
+    attention mask over the prompt; transformers' causal mask then lets the query
+    at position p see keys 0..p (the prefix and the suffix up to itself). Here
+    the suffix's own K/V are read from the pool like the prefix (they are
+    written there before attention), so new token i of a sequence with context
+    length L and n new tokens sits at position p = L - n + i and attends to
+    pool rows 0..p. Rows are gathered as naive_reference_paged_attention
+    gathers them (paged_attention.py:58-69); query head h reads kv head
+    h // group (:73-76). Returns compute_dtype.
+    """
+    num_tokens, num_q_heads, head_dim = q.shape
+    num_kv_heads = k_cache.shape[2]
+    assert num_q_heads % num_kv_heads == 0
+    group = num_q_heads // num_kv_heads
+    bs = k_cache.shape[1]
+    out = torch.zeros((num_tokens, num_q_heads, head_dim), dtype=compute_dtype)
+    kv_head = torch.arange(num_q_heads) // group
+    row = 0
+    for s_idx, (L, n) in enumerate(zip(seq_lens, query_lens)):
+        L, n = int(L), int(n)
+        assert 0 <= n <= L
+        if n == 0:
+            continue
+        nb = (L + bs - 1) // bs
+        ids = torch.tensor(list(block_tables[s_idx])[:nb], dtype=torch.long)
+        k = k_cache[ids].reshape(nb * bs, num_kv_heads, head_dim)[:L].to(compute_dtype)
+        v = v_cache[ids].reshape(nb * bs, num_kv_heads, head_dim)[:L].to(compute_dtype)
+        qs = q[row:row + n].to(compute_dtype)                    # [n, Hq, D]
+        scores = torch.einsum("nhd,shd->hns", qs, k[:, kv_head]) * scale   # [Hq, n, L]
+        pos = torch.arange(L - n, L).unsqueeze(1)                 # [n, 1]
+        visible = torch.arange(L).unsqueeze(0) <= pos             # [n, L]
+        scores = scores.masked_fill(~visible, float("-inf"))
+        probs = torch.softmax(scores, dim=-1)
+        out[row:row + n] = torch.einsum("hns,shd->nhd", probs, v[:, kv_head])
+        row += n
+    return out

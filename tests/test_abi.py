@@ -22,6 +22,7 @@ def _declared_symbols():
 def test_header_declares_the_entry_points():
     names = _declared_symbols()
     for n in ["pa_decode_batched_f16", "pa_decode_v1_f16", "pa_decode_v2_f16", "pa_kv_write_f16",
+              "pa_prefill_copy_f16", "pa_rope_kv_write_f16", "pa_prefill_attention_f16",
               "pa_last_error", "pa_abi_version"]:
         assert n in names
 
@@ -89,6 +90,28 @@ def test_kv_write_argument_errors():
                              _strides(4, 1), 16, 0, 4, 2, 64, 16, 100, 4, None)
     assert rc == _native.PA_ERR_ARG
     assert b"null" in lib.pa_last_error()
+
+
+def _prefill_call(lib, head_dim=64, nq=14, nkv=2, q=16, qstart=16, qstr=(896, 64, 1), maxq=8,
+                  ntok=32):
+    kstr = (2048, 128, 64, 1)
+    return lib.pa_prefill_attention_f16(
+        q, _strides(*qstr), 16, _strides(*kstr), 16, _strides(*kstr), 16, _strides(64, 1), 16,
+        qstart, maxq, 16, _strides(896, 64, 1), 4, ntok, nq, nkv, head_dim, 16, 100, 64, 0.125,
+        None)
+
+
+def test_prefill_argument_errors():
+    lib = _native.load()
+    assert _prefill_call(lib, head_dim=48) == _native.PA_ERR_UNSUPPORTED
+    assert _prefill_call(lib, nq=15) == _native.PA_ERR_ARG
+    assert _prefill_call(lib, qstart=0) == _native.PA_ERR_ARG
+    assert b"null" in lib.pa_last_error()
+    assert _prefill_call(lib, qstr=(900, 64, 1)) == _native.PA_ERR_ARG  # token stride not 8-aligned
+    assert _prefill_call(lib, maxq=-1) == _native.PA_ERR_ARG
+    # Nothing to compute: no launch, no pointer is touched.
+    assert _prefill_call(lib, q=0, qstart=0, maxq=0) == _native.PA_OK
+    assert _prefill_call(lib, q=0, qstart=0, ntok=0) == _native.PA_OK
 
 
 def test_error_text_is_thread_local():

@@ -175,7 +175,7 @@ using namespace pa;
 
 extern "C" {
 
-int pa_abi_version(void) { return 3; }
+int pa_abi_version(void) { return 4; }
 
 const char* pa_last_error(void) { return g_error.c_str(); }
 
@@ -599,6 +599,77 @@ int pa_rope_kv_write_f16(const void* q, const int64_t q_strides[3], const void* 
                    rows16(q_out, a.qo_b, a.qo_h, 1) && rows16(k_cache, a.kc_sb, a.kc_st, 1) &&
                    a.kc_sh % 8 == 0 && rows16(v_cache, a.vc_sb, a.vc_st, 1) && a.vc_sh % 8 == 0;
   return finish_launch(launch_rope_kv_write(a, vec, (hipStream_t)stream));
+}
+
+int pa_prefill_attention_f16(const void* q, const int64_t q_strides[3], const void* k_cache,
+                             const int64_t k_strides[4], const void* v_cache,
+                             const int64_t v_strides[4], const int32_t* block_tables,
+                             const int64_t bt_strides[2], const int32_t* seq_lens,
+                             const int32_t* query_start_loc, int max_query_len, void* out,
+                             const int64_t out_strides[3], int num_seqs, int num_tokens,
+                             int num_q_heads, int num_kv_heads, int head_dim, int block_size,
+                             int num_blocks, int max_blocks_per_seq, float scale, void* stream) {
+  clear_error();
+  if (num_seqs < 0 || num_tokens < 0 || max_query_len < 0) {
+    set_error("num_seqs, num_tokens and max_query_len must be >= 0");
+    return PA_ERR_ARG;
+  }
+  if (num_seqs == 0 || num_tokens == 0 || max_query_len == 0) return PA_OK;
+  int rc = check_common(q, k_cache, v_cache, out, k_strides, v_strides, num_q_heads,
+                        num_kv_heads, head_dim, block_size, num_blocks);
+  if (rc) return rc;
+  if (!q_strides || !out_strides || !bt_strides || !block_tables || !seq_lens ||
+      !query_start_loc) {
+    set_error("null pointer argument");
+    return PA_ERR_ARG;
+  }
+  if (q_strides[2] != 1 || out_strides[2] != 1 || q_strides[0] % 8 || q_strides[1] % 8 ||
+      out_strides[0] % 4 || out_strides[1] % 4) {
+    set_error("q needs unit head_dim stride and 8-element aligned token/head strides; "
+              "out unit head_dim stride and 4-element aligned strides");
+    return PA_ERR_ARG;
+  }
+  if (max_blocks_per_seq <= 0) {
+    set_error("block table needs at least one column");
+    return PA_ERR_ARG;
+  }
+  const int g = num_q_heads / num_kv_heads;
+  const int64_t col_blocks = ((int64_t)max_query_len * g + 63) / 64;
+  const int64_t grid = col_blocks * num_seqs * num_kv_heads;
+  if (grid > 0x7fffffff) {
+    set_error("%lld workgroups exceed the grid limit", (long long)grid);
+    return PA_ERR_UNSUPPORTED;
+  }
+  PrefillAttnArgs a{};
+  a.q = (const f16*)q;
+  a.q_st = q_strides[0];
+  a.q_sh = q_strides[1];
+  a.k = (const f16*)k_cache;
+  a.k_sb = k_strides[0];
+  a.k_st = k_strides[1];
+  a.k_sh = k_strides[2];
+  a.v = (const f16*)v_cache;
+  a.v_sb = v_strides[0];
+  a.v_st = v_strides[1];
+  a.v_sh = v_strides[2];
+  a.bt = block_tables;
+  a.bt_sb = bt_strides[0];
+  a.bt_sk = bt_strides[1];
+  a.lens = seq_lens;
+  a.qstart = query_start_loc;
+  a.out = (f16*)out;
+  a.o_st = out_strides[0];
+  a.o_sh = out_strides[1];
+  a.num_seqs = num_seqs;
+  a.num_tokens = num_tokens;
+  a.hkv = num_kv_heads;
+  a.g = g;
+  a.bs = block_size;
+  a.num_blocks = num_blocks;
+  a.max_blocks = max_blocks_per_seq;
+  a.col_blocks = (int)col_blocks;
+  a.scale_log2 = scale * kLog2e;
+  return finish_launch(launch_prefill_attn(a, head_dim, (hipStream_t)stream));
 }
 
 }  // extern "C"

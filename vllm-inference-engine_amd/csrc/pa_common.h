@@ -124,6 +124,27 @@ struct RopeKVArgs {
   int num_seqs, hq, hkv, D, bs, num_blocks, max_blocks;
 };
 
+// Argument bundle of the paged prefill attention: new query rows of all
+// sequences packed [num_tokens, Hq, D] (sequence b owns rows qstart[b] ..
+// qstart[b + 1]), each attending causally over its first lens[b] pool rows.
+struct PrefillAttnArgs {
+  const f16* q;
+  int64_t q_st, q_sh;
+  const f16* k;
+  int64_t k_sb, k_st, k_sh;
+  const f16* v;
+  int64_t v_sb, v_st, v_sh;
+  const int32_t* bt;
+  int64_t bt_sb, bt_sk;
+  const int32_t* lens;    // context length after the new tokens
+  const int32_t* qstart;  // [num_seqs + 1] first query row of each sequence
+  f16* out;
+  int64_t o_st, o_sh;
+  int num_seqs, num_tokens, hkv, g, bs, num_blocks, max_blocks;
+  int col_blocks;  // column blocks per (sequence, kv head): ceil(max_query_len * g / 64)
+  float scale_log2;
+};
+
 // Launchers (defined next to their kernels).
 hipError_t launch_decode_split(const DecodeArgs& a, int D, int num_seqs, hipStream_t s);
 hipError_t launch_decode_v1(const DecodeArgs& a, int D, hipStream_t s);
@@ -131,6 +152,7 @@ hipError_t launch_kv_write(const KVWriteArgs& a, bool vec, hipStream_t s);
 hipError_t launch_prefill_copy(const PrefillCopyArgs& a, bool vec, hipStream_t s);
 hipError_t launch_rope_kv_write(const RopeKVArgs& a, bool vec, hipStream_t s);
 hipError_t launch_decode_streamk(const DecodeArgs& a, int D, hipStream_t s);
+hipError_t launch_prefill_attn(const PrefillAttnArgs& a, int D, hipStream_t s);
 int streamk_head_group(int num_kv_heads, int D);
 
 // Length of sequence b clamped to [0, max_blocks * bs].

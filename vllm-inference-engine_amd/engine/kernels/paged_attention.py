@@ -33,6 +33,7 @@ __all__ = [
     "paged_attention_decode_v1",
     "paged_attention_decode_v2",
     "paged_attention_decode_batched",
+    "paged_attention_prefill",
     "pad_block_tables",
 ]
 
@@ -75,10 +76,11 @@ def paged_attention_decode_batched(
 ) -> torch.Tensor:
     """Batched GQA paged decode attention (reference paged_attention.py:634-698).
 
-    One launch covers every sequence; each (sequence, kv head) is cut into
-    split-K partitions processed by one wavefront each, with a log-sum-exp
-    merge when a sequence spans several partitions. Asynchronous on the
-    current stream, like the Triton launch it replaces.
+    One persistent launch covers every sequence: the (sequence, kv-head group)
+    pairs are split into equal contiguous ranges of 16-token tiles, one per
+    compute unit, and a pair cut by a range boundary is merged by log-sum-exp
+    inside the same launch. Asynchronous on the current stream, like the
+    Triton launch it replaces; repeated calls return the same bits.
     """
     assert q.is_cuda and k_cache.is_cuda and v_cache.is_cuda
     assert block_tables.is_cuda and seq_lens.is_cuda
@@ -120,6 +122,65 @@ def paged_attention_decode_batched(
             float(scale), _native.workspace(ws_bytes, dev, stream, _native.WS_DECODE), ws_bytes,
             stream)
     _native.check(status, "pa_decode_batched_f16")
+    return out
+
+
+def paged_attention_prefill(
+    q: torch.Tensor,                # [num_tokens, num_q_heads, head_dim] (fp16, cuda)
+    k_cache: torch.Tensor,          # [num_blocks, block_size, num_kv_heads, head_dim]
+    v_cache: torch.Tensor,
+    block_tables: torch.Tensor,     # [num_seqs, max_blocks_per_seq] (int32, cuda)
+    seq_lens: torch.Tensor,         # [num_seqs] (int32, cuda): context length after the new tokens
+    query_start_loc: torch.Tensor,  # [num_seqs + 1] (int32, cuda): first q row of each sequence
+    max_query_len: int,
+    scale: float,
+) -> torch.Tensor:
+    """Causal attention of each sequence's new tokens over its paged context.
+
+    The attention of the reference's "full" prefix-cache prefill
+    (engine/kernels/paged_attention_integration.py:459-482): the uncached prompt
+    suffix attends over the cached prefix blocks (:364-392) and itself. The
+    new tokens' K/V must already be in the pool. Sequence b owns q rows
+    query_start_loc[b] .. query_start_loc[b+1]-1; its new token i sits at
+    position seq_lens[b] - n_b + i and sees pool positions 0 .. that position.
+    max_query_len (a host int, at least every n_b) sizes the grid, so the
+    call never reads device memory on the host. Asynchronous on the current
+    stream; no workspace.
+    """
+    assert q.is_cuda and k_cache.is_cuda and v_cache.is_cuda
+    assert block_tables.is_cuda and seq_lens.is_cuda and query_start_loc.is_cuda
+    assert q.dtype == torch.float16 and k_cache.dtype == torch.float16 and v_cache.dtype == torch.float16
+    assert block_tables.dtype == torch.int32 and seq_lens.dtype == torch.int32
+    assert query_start_loc.dtype == torch.int32
+    num_tokens, num_q_heads, head_dim = q.shape
+    num_blocks, block_size, num_kv_heads, head_dim_k = k_cache.shape
+    assert head_dim == head_dim_k, f"Head dimensions must match: {head_dim} vs {head_dim_k}"
+    assert num_q_heads % num_kv_heads == 0, (
+        f"num_q_heads ({num_q_heads}) must be divisible by num_kv_heads ({num_kv_heads})"
+    )
+    num_seqs = seq_lens.shape[0]
+    assert block_tables.dim() == 2 and block_tables.shape[0] == num_seqs
+    assert query_start_loc.dim() == 1 and query_start_loc.shape[0] == num_seqs + 1
+    assert v_cache.shape == k_cache.shape, "k_cache and v_cache must have the same shape"
+    assert max_query_len >= 0
+
+    q = _q_ready(q)
+    out = torch.empty_like(q)
+    if num_seqs == 0 or num_tokens == 0 or max_query_len == 0:
+        return out
+    lib = _native.load()
+    dev = q.device
+    with _on_device(dev):
+        status = lib.pa_prefill_attention_f16(
+            q.data_ptr(), _native.strides_of(q),
+            k_cache.data_ptr(), _native.strides_of(k_cache),
+            v_cache.data_ptr(), _native.strides_of(v_cache),
+            block_tables.data_ptr(), _native.strides_of(block_tables),
+            seq_lens.data_ptr(), query_start_loc.data_ptr(), int(max_query_len),
+            out.data_ptr(), _native.strides_of(out),
+            num_seqs, num_tokens, num_q_heads, num_kv_heads, head_dim, block_size, num_blocks,
+            block_tables.shape[1], float(scale), _native.stream_handle(dev))
+    _native.check(status, "pa_prefill_attention_f16")
     return out
 
 
