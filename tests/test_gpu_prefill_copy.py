@@ -92,10 +92,12 @@ class FakePrefillModel:
 
 
 def _runner(model, mode, device):
+    """The fixture model has no attention modules to patch, so "full" mode runs the
+    reference's own DynamicCache path (paged_prefill=False), which these fixtures pin."""
     from engine.kernels.paged_attention_integration import KernelPagedManualDecode
 
     return KernelPagedManualDecode(model=model, block_size=2, num_blocks=2, device=str(device),
-                                   dtype=torch.float16, prefix_mode=mode)
+                                   dtype=torch.float16, prefix_mode=mode, paged_prefill=False)
 
 
 def test_prefill_keeps_hit_blocks_and_copies_only_owned_blocks(cuda_device):

@@ -10,6 +10,10 @@ engine/kernels/paged_attention_integration.py:
 
   * KernelPagedManualDecode (reference :211-731): prefill into the pool,
     batched decode steps, single-sequence greedy generation.
+  * PagedPrefillContext / paged_prefill_attention_forward: the "full"
+    prefix-cache prefill (reference :459-482) without the DynamicCache copy of
+    the cached blocks (:364-392): each layer writes the suffix's K/V into its
+    blocks and runs the paged prefill attention kernel over the pool.
 
 The reference writes K/V with a Python loop of two index_put calls per sequence
 and a device-to-host `.item()` per sequence per layer (:148-161). Here the
@@ -29,7 +33,12 @@ import torch
 import torch.nn as nn
 
 from . import _native
-from .paged_attention import _on_device, pad_block_tables, paged_attention_decode_batched
+from .paged_attention import (
+    _on_device,
+    pad_block_tables,
+    paged_attention_decode_batched,
+    paged_attention_prefill,
+)
 
 __all__ = [
     "PagedAttentionContext",
@@ -37,6 +46,8 @@ __all__ = [
     "paged_rope_kv_write",
     "paged_prefill_copy",
     "paged_decode_attention_forward",
+    "paged_prefill_attention_forward",
+    "PagedPrefillContext",
     "patch_paged_attention",
     "KernelPagedManualDecode",
 ]
@@ -230,6 +241,34 @@ class PagedAttentionContext:
         return ctx
 
 
+class PagedPrefillContext:
+    """Metadata of one sequence's paged prefill: the prompt after `cached_tokens` cached tokens.
+
+    The new tokens' K/V go to the sequence's blocks from cached_tokens // block_size
+    on (whole blocks, rows past the prompt zeroed, as the reference's
+    _copy_prefill_kv with skip_blocks writes them, integration.py:278-326); the
+    attention reads the cached blocks and those new rows from the pool.
+    """
+
+    is_decode = False
+    is_prefill = True
+
+    def __init__(self, pool: Any, block_ids: List[int], cached_tokens: int, prompt_len: int,
+                 block_size: int):
+        assert cached_tokens % block_size == 0 and 0 <= cached_tokens < prompt_len
+        nb = (prompt_len + block_size - 1) // block_size
+        assert len(block_ids) >= nb, "block table shorter than the prompt"
+        dev = pool.device
+        self.pool = pool
+        self.block_size = block_size
+        self.num_new = prompt_len - cached_tokens
+        self.block_tables = torch.tensor([list(block_ids[:nb])], dtype=torch.int32, device=dev)
+        self.write_ids = torch.tensor(list(block_ids[cached_tokens // block_size:nb]),
+                                      dtype=torch.int32, device=dev)
+        self.seq_lens = torch.tensor([prompt_len], dtype=torch.int32, device=dev)
+        self.query_start_loc = torch.tensor([0, self.num_new], dtype=torch.int32, device=dev)
+
+
 def paged_decode_attention_forward(
     self: nn.Module,
     hidden_states: torch.Tensor,
@@ -247,6 +286,9 @@ def paged_decode_attention_forward(
     reference); then o_proj.
     """
     ctx: Optional[PagedAttentionContext] = getattr(self, "_paged_attention_context", None)
+    if ctx is not None and getattr(ctx, "is_prefill", False):
+        return paged_prefill_attention_forward(self, hidden_states, position_embeddings,
+                                               attention_mask, past_key_values, **kwargs)
     if ctx is None or not ctx.is_decode:
         orig_forward = getattr(self, "_orig_attention_forward", None)
         if orig_forward is not None:
@@ -298,6 +340,51 @@ def paged_decode_attention_forward(
     attn_output = attn_output.reshape(*input_shape, -1).contiguous()
     attn_output = self.o_proj(attn_output)
     return attn_output, None
+
+
+def paged_prefill_attention_forward(
+    self: nn.Module,
+    hidden_states: torch.Tensor,
+    position_embeddings: Tuple[torch.Tensor, torch.Tensor],
+    attention_mask: Optional[torch.Tensor] = None,
+    past_key_values: Any = None,
+    **kwargs: Any,
+) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
+    """Attention forward for a prompt suffix of one sequence over its cached prefix blocks.
+
+    Replaces the reference's "full" prefix-cache prefill attention
+    (integration.py:459-482), which copies the cached blocks of every layer
+    into a DynamicCache (:364-392) and runs transformers' causal attention over
+    prefix + suffix. Here: q/k/v projections; RoPE with transformers'
+    apply_rotary_pos_emb (the reference's, :108-109); the suffix's K/V written
+    into the sequence's own blocks with paged_prefill_copy; causal paged
+    prefill attention over the pool; o_proj. The causal mask is the kernel's
+    (new token i at position cached + i sees pool positions 0 .. cached + i),
+    so `attention_mask` is not used.
+    """
+    from transformers.models.qwen2.modeling_qwen2 import apply_rotary_pos_emb
+
+    ctx: PagedPrefillContext = self._paged_attention_context
+    input_shape = hidden_states.shape[:-1]  # [1, n]
+    assert input_shape[0] == 1 and input_shape[1] == ctx.num_new
+    hidden_shape = (*input_shape, -1, self.head_dim)
+    query_states = self.q_proj(hidden_states).view(hidden_shape).transpose(1, 2)
+    key_states = self.k_proj(hidden_states).view(hidden_shape).transpose(1, 2)
+    value_states = self.v_proj(hidden_states).view(hidden_shape).transpose(1, 2)
+    cos, sin = position_embeddings
+    query_states, key_states = apply_rotary_pos_emb(query_states, key_states, cos, sin)
+
+    scale = self.scaling if hasattr(self, "scaling") else 1.0 / math.sqrt(self.head_dim)
+    k_cache = ctx.pool.k_cache[self.layer_idx]
+    v_cache = ctx.pool.v_cache[self.layer_idx]
+    # [1, H, n, D] -> [n, H, D] views; the kernels take any token/head strides.
+    paged_prefill_copy(key_states[0].transpose(0, 1), value_states[0].transpose(0, 1),
+                       k_cache, v_cache, ctx.write_ids, ctx.num_new)
+    attn = paged_attention_prefill(query_states[0].transpose(0, 1), k_cache, v_cache,
+                                   ctx.block_tables, ctx.seq_lens, ctx.query_start_loc,
+                                   ctx.num_new, scale)
+    attn_output = attn.reshape(*input_shape, -1).contiguous()
+    return self.o_proj(attn_output), None
 
 
 @contextmanager
@@ -452,7 +539,10 @@ class KernelPagedManualDecode:
 
     prefill(seq): Hugging Face forward over the prompt, then the owned K/V
     blocks are written into the pool with paged_prefill_copy (prefix modes
-    "off", "share", "full" as in the reference). decode_step(seqs): one
+    "off", "share", "full" as in the reference). In "full" mode with a cached
+    prefix (and paged_prefill, the default) only the suffix is forwarded, with
+    paged_prefill_attention_forward patched in: its K/V go straight into the
+    sequence's blocks and its attention reads the prefix from the pool. decode_step(seqs): one
     batched forward with paged_decode_attention_forward patched into every
     attention module, so each layer runs the fused RoPE + K/V write and the
     batched paged attention kernel. With use_graphs (the default) the forward
@@ -475,6 +565,7 @@ class KernelPagedManualDecode:
         debug_prefix_cache: bool = False,
         prefix_mode: str = "off",
         use_graphs: bool = True,
+        paged_prefill: bool = True,
     ):
         from ..memory.block_pool import FreeListAllocator, PhysicalBlockPool
 
@@ -507,6 +598,10 @@ class KernelPagedManualDecode:
         # table width rounded up to a multiple of 64 blocks).
         self.use_graphs = use_graphs
         self._graphs: dict = {}
+        # "full" prefix mode: forward the suffix through the paged prefill
+        # kernel over the pool (True) or, as the reference does, through
+        # transformers' attention over a DynamicCache copy of the prefix.
+        self.paged_prefill = paged_prefill
 
     # -- prefill -----------------------------------------------------------------
     def _copy_prefill_kv(self, pkv: Any, block_table: Any, prompt_len: int, skip_blocks: int = 0) -> None:
@@ -568,17 +663,27 @@ class KernelPagedManualDecode:
                              f"prompt_len={prompt_len} (block_size={self.block_size}).")
         if cached // self.block_size > len(block_table.physical_block_ids):
             raise ValueError("num_cached_tokens exceeds the number of blocks in the sequence table.")
-        if self.prefix_mode == "full" and cached:
-            prefix = self._build_cached_prefix(block_table, cached)
-            out = self.model(
-                input_ids=input_ids[:, cached:],
-                attention_mask=torch.ones((1, prompt_len), dtype=torch.long, device=self.device),
-                position_ids=torch.arange(cached, prompt_len, device=self.device).unsqueeze(0),
-                past_key_values=prefix, use_cache=True, logits_to_keep=1)
+        positions = torch.arange(cached, prompt_len, device=self.device).unsqueeze(0)
+        if self.prefix_mode == "full" and cached and self.paged_prefill and cached < prompt_len:
+            # Each layer writes the suffix's K/V into the sequence's own blocks
+            # and attends over the pool; nothing is left to copy afterwards.
+            ctx = PagedPrefillContext(self.pool, list(block_table.physical_block_ids), cached,
+                                      prompt_len, self.block_size)
+            with patch_paged_attention(self.model, ctx):
+                out = self.model(input_ids=input_ids[:, cached:], position_ids=positions,
+                                 use_cache=False, logits_to_keep=1)
         else:
-            out = self.model(input_ids=input_ids, use_cache=True, logits_to_keep=1)
-        self._copy_prefill_kv(out.past_key_values, block_table, prompt_len,
-                              skip_blocks=cached // self.block_size)
+            if self.prefix_mode == "full" and cached:
+                prefix = self._build_cached_prefix(block_table, cached)
+                out = self.model(
+                    input_ids=input_ids[:, cached:],
+                    attention_mask=torch.ones((1, prompt_len), dtype=torch.long, device=self.device),
+                    position_ids=positions, past_key_values=prefix, use_cache=True,
+                    logits_to_keep=1)
+            else:
+                out = self.model(input_ids=input_ids, use_cache=True, logits_to_keep=1)
+            self._copy_prefill_kv(out.past_key_values, block_table, prompt_len,
+                                  skip_blocks=cached // self.block_size)
         logits = out.logits[:, -1, :]
         top2 = torch.topk(logits[0], k=2).values.double()
         # float64 holds every token id exactly; one transfer for id and margin.
