@@ -208,7 +208,8 @@ PA_API int pa_rope_kv_write_f16(const void* q, const int64_t q_strides[3], const
  * softmax(scale * q k^T) v over pool positions 0 .. p, query head h reading kv
  * head h / (num_q_heads / num_kv_heads). max_query_len must be at least every
  * n_b (rows past it are not computed); rows with p < 0 are written as zeros;
- * rows outside every sequence's range are not written. Needs no workspace.
+ * rows outside every sequence's range are not written. scale must be positive
+ * and finite. Needs no workspace.
  */
 PA_API int pa_prefill_attention_f16(const void* q, const int64_t q_strides[3],
                                     const void* k_cache, const int64_t k_strides[4],

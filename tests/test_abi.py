@@ -93,11 +93,11 @@ def test_kv_write_argument_errors():
 
 
 def _prefill_call(lib, head_dim=64, nq=14, nkv=2, q=16, qstart=16, qstr=(896, 64, 1), maxq=8,
-                  ntok=32):
+                  ntok=32, scale=0.125):
     kstr = (2048, 128, 64, 1)
     return lib.pa_prefill_attention_f16(
         q, _strides(*qstr), 16, _strides(*kstr), 16, _strides(*kstr), 16, _strides(64, 1), 16,
-        qstart, maxq, 16, _strides(896, 64, 1), 4, ntok, nq, nkv, head_dim, 16, 100, 64, 0.125,
+        qstart, maxq, 16, _strides(896, 64, 1), 4, ntok, nq, nkv, head_dim, 16, 100, 64, scale,
         None)
 
 
@@ -109,6 +109,9 @@ def test_prefill_argument_errors():
     assert b"null" in lib.pa_last_error()
     assert _prefill_call(lib, qstr=(900, 64, 1)) == _native.PA_ERR_ARG  # token stride not 8-aligned
     assert _prefill_call(lib, maxq=-1) == _native.PA_ERR_ARG
+    assert _prefill_call(lib, scale=0.0) == _native.PA_ERR_ARG
+    assert _prefill_call(lib, scale=-0.125) == _native.PA_ERR_ARG
+    assert b"scale" in lib.pa_last_error()
     # Nothing to compute: no launch, no pointer is touched.
     assert _prefill_call(lib, q=0, qstart=0, maxq=0) == _native.PA_OK
     assert _prefill_call(lib, q=0, qstart=0, ntok=0) == _native.PA_OK

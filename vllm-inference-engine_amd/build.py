@@ -41,6 +41,14 @@ HIPCC_FLAGS = [
 ]
 
 
+# Extra flags per source file. The prefill attention kernel rescales its MFMA
+# accumulators with vector ops; in the accumulator-register form every rescale
+# copies them out and back, so its MFMAs use the VGPR form.
+FILE_FLAGS = {
+    "pa_prefill.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+}
+
+
 def _hipcc() -> str:
     exe = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
     if not Path(exe).exists():
@@ -54,7 +62,7 @@ def _sources() -> list[Path]:
 
 def _compile_one(src: Path) -> Path:
     obj = BUILD_DIR / (src.stem + ".o")
-    cmd = [_hipcc(), *HIPCC_FLAGS, "-c", str(src), "-o", str(obj)]
+    cmd = [_hipcc(), *HIPCC_FLAGS, *FILE_FLAGS.get(src.name, []), "-c", str(src), "-o", str(obj)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"hipcc failed on {src.name}:\n{proc.stdout}\n{proc.stderr}")

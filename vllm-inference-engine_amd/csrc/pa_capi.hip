@@ -633,8 +633,13 @@ int pa_prefill_attention_f16(const void* q, const int64_t q_strides[3], const vo
     set_error("block table needs at least one column");
     return PA_ERR_ARG;
   }
+  if (!(scale > 0.f) || scale == __builtin_huge_valf()) {
+    set_error("scale must be positive and finite");
+    return PA_ERR_ARG;
+  }
   const int g = num_q_heads / num_kv_heads;
-  const int64_t col_blocks = ((int64_t)max_query_len * g + 63) / 64;
+  const int cols = prefill_cols_per_wg(head_dim);
+  const int64_t col_blocks = ((int64_t)max_query_len * g + cols - 1) / cols;
   const int64_t grid = col_blocks * num_seqs * num_kv_heads;
   if (grid > 0x7fffffff) {
     set_error("%lld workgroups exceed the grid limit", (long long)grid);

@@ -7,6 +7,7 @@
 namespace pa {
 
 typedef _Float16 f16;
+typedef f16 f16x2 __attribute__((ext_vector_type(2)));
 typedef f16 f16x4 __attribute__((ext_vector_type(4)));
 typedef f16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -141,9 +142,15 @@ struct PrefillAttnArgs {
   f16* out;
   int64_t o_st, o_sh;
   int num_seqs, num_tokens, hkv, g, bs, num_blocks, max_blocks;
-  int col_blocks;  // column blocks per (sequence, kv head): ceil(max_query_len * g / 64)
+  int col_blocks;  // column blocks per (sequence, kv head): ceil(max_query_len * g / columns)
   float scale_log2;
 };
+
+// Column groups of 16 (token, query head) columns each prefill wavefront
+// takes (four wavefronts per workgroup): two below head_dim 256, where the
+// registers allow it, so each K and V operand read from LDS feeds two MFMAs.
+__host__ __device__ constexpr int prefill_col_groups(int D) { return D <= 128 ? 2 : 1; }
+__host__ __device__ constexpr int prefill_cols_per_wg(int D) { return 64 * prefill_col_groups(D); }
 
 // Launchers (defined next to their kernels).
 hipError_t launch_decode_split(const DecodeArgs& a, int D, int num_seqs, hipStream_t s);

@@ -26,21 +26,27 @@ namespace pa {
 
 using namespace tiles;
 
-template <int D>
+template <int D, int BS, int CG>
 __global__ __launch_bounds__(256) void prefill_attn_kernel(PrefillAttnArgs a) {
   constexpr int NW = 4;
-  constexpr int COLS = 16 * NW;  // columns per workgroup
-  constexpr int KT = 64;         // keys per staged tile
-  constexpr int NS = KT / 16;    // 16-key sub-tiles per tile
+  constexpr int COLS = 16 * CG * NW;  // columns per workgroup
+  constexpr int KT = 64;              // keys per staged tile
+  constexpr int NS = KT / 16;         // 16-key sub-tiles per tile
   constexpr int NC = D / 32;
   constexpr int ND = D / 16;
-  constexpr int LS = D + 8;      // LDS row stride in halves
-  constexpr int CPR = D / 8;     // 16-byte pieces per key row of one head
+  constexpr int LS = D + 8;           // LDS row stride in halves
+  constexpr int CPR = D / 8;          // 16-byte pieces per key row of one head
   constexpr int PER = KT * CPR / (64 * NW);
+  constexpr int BUF = KT * LS;        // halves of one staged K (or V) tile
+  // Lazy rescaling: the running maximum is raised only when a tile's maximum
+  // exceeds it by more than this (exp2 units), so probabilities stay <= 2^8
+  // and most tiles skip the rescale of the accumulators.
+  constexpr float kLazy = 8.f;
   static_assert(PER * 64 * NW == KT * CPR, "a tile must split evenly over the workgroup");
+  static_assert(NS % 2 == 0, "sub-tiles are paired for the P V products");
 
-  __shared__ __attribute__((aligned(16))) f16 ks[KT * LS];
-  __shared__ __attribute__((aligned(16))) f16 vs[KT * LS];
+  __shared__ __attribute__((aligned(16))) f16 ks[2 * BUF];
+  __shared__ __attribute__((aligned(16))) f16 vs[2 * BUF];
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -66,52 +72,67 @@ __global__ __launch_bounds__(256) void prefill_attn_kernel(PrefillAttnArgs a) {
   const int cap = a.max_blocks * a.bs;
   int L = a.lens[b];
   L = L < 0 ? 0 : (L > cap ? cap : L);
-  const int pos0 = L - qlen;                  // position of the first new token
-  const int kmax = pos0 + clast / a.g + 1;    // keys [0, kmax) are read
-  const int pmin = pos0 + cfirst / a.g;       // every column sees keys [0, pmin]
+  const int pos0 = L - qlen;                // position of the first new token
+  const int kmax = pos0 + clast / a.g + 1;  // keys [0, kmax) are read
+  const int pmin = pos0 + cfirst / a.g;     // every column sees keys [0, pmin]
 
-  // This lane's column; columns past the list compute as the last valid one
-  // and are not stored.
-  const int col = cfirst + wave * 16 + row;
-  const bool col_ok = col < ncols;
-  const int cc = col_ok ? col : clast;
-  const int t = cc / a.g;
-  const int j = cc - t * a.g;
-  const int pos = pos0 + t;
-  f16* op = a.out + (int64_t)(q0 + t) * a.o_st + (int64_t)(h * a.g + j) * a.o_sh + grp * 4;
-
-  if (kmax <= 0) {  // context shorter than the new tokens: no key is visible to any column
-    if (col_ok) {
+  // This lane's columns (one per column group); columns past the list compute
+  // as the last valid one and are not stored.
+  bool col_ok[CG];
+  int pos[CG], pos_c[CG];
+  f16* op[CG];
+  f16x8 qf[CG][NC];
 #pragma unroll
-      for (int nd = 0; nd < ND; ++nd) *reinterpret_cast<f16x4*>(op + nd * 16) = f16x4{0, 0, 0, 0};
-    }
-    return;
-  }
-  const int pos_c = pos < 0 ? 0 : pos;  // such columns are written as zeros below
-
-  f16x8 qf[NC];
-  {
+  for (int cg = 0; cg < CG; ++cg) {
+    const int col = cfirst + (wave * CG + cg) * 16 + row;
+    col_ok[cg] = col < ncols;
+    const int cc = col_ok[cg] ? col : clast;
+    const int t = cc / a.g;
+    const int j = cc - t * a.g;
+    pos[cg] = pos0 + t;
+    pos_c[cg] = pos[cg] < 0 ? 0 : pos[cg];  // such columns are written as zeros below
+    op[cg] = a.out + (int64_t)(q0 + t) * a.o_st + (int64_t)(h * a.g + j) * a.o_sh + grp * 4;
     const f16* qp = a.q + (int64_t)(q0 + t) * a.q_st + (int64_t)(h * a.g + j) * a.q_sh + grp * 8;
 #pragma unroll
-    for (int c = 0; c < NC; ++c) qf[c] = *reinterpret_cast<const f16x8*>(qp + 32 * c);
+    for (int c = 0; c < NC; ++c) qf[cg][c] = *reinterpret_cast<const f16x8*>(qp + 32 * c);
+  }
+
+  if (kmax <= 0) {  // context shorter than the new tokens: no key is visible to any column
+#pragma unroll
+    for (int cg = 0; cg < CG; ++cg)
+      if (col_ok[cg]) {
+#pragma unroll
+        for (int nd = 0; nd < ND; ++nd)
+          *reinterpret_cast<f16x4*>(op[cg] + nd * 16) = f16x4{0, 0, 0, 0};
+      }
+    return;
   }
 
   const int32_t* btrow = a.bt + (int64_t)b * a.bt_sb;
   const f16* kbase = a.k + (int64_t)h * a.k_sh;
   const f16* vbase = a.v + (int64_t)h * a.v_sh;
+  const int bs = BS > 0 ? BS : a.bs;
   u32x4 kr[PER], vr[PER];
+  int ids[PER];
   // Piece f = 256 i + tid of a tile is key row f / CPR, halves (f % CPR) * 8.
-  auto fetch = [&](int kt) {
+  // The block ids of a tile are loaded one tile before its K/V, so a K/V load
+  // never waits on the table read it depends on.
+  auto fetch_ids = [&](int kt) {
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int key = kt * KT + (i * 64 * NW + tid) / CPR;
+      ids[i] = key < kmax ? btrow[(int64_t)(key / bs) * a.bt_sk] : 0;
+    }
+  };
+  auto fetch_kv = [&](int kt) {
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
       const int f = i * 64 * NW + tid;
-      const int r = f / CPR;
       const int c8 = (f % CPR) * 8;
-      const int key = kt * KT + r;
+      const int key = kt * KT + f / CPR;
       if (key < kmax) {
-        int id = btrow[(int64_t)(key / a.bs) * a.bt_sk];
-        id = min(max(id, 0), a.num_blocks - 1);
-        const int64_t off = key % a.bs;
+        const int64_t id = min(max(ids[i], 0), a.num_blocks - 1);
+        const int64_t off = key % bs;
         kr[i] = *reinterpret_cast<const u32x4*>(kbase + id * a.k_sb + off * a.k_st + c8);
         vr[i] = *reinterpret_cast<const u32x4*>(vbase + id * a.v_sb + off * a.v_st + c8);
       } else {
@@ -122,109 +143,154 @@ __global__ __launch_bounds__(256) void prefill_attn_kernel(PrefillAttnArgs a) {
       }
     }
   };
-  auto stash = [&]() {
+  auto stash = [&](int buf) {
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
       const int f = i * 64 * NW + tid;
       const int r = f / CPR;
       const int c8 = (f % CPR) * 8;
-      *reinterpret_cast<u32x4*>(&ks[r * LS + c8]) = kr[i];
-      *reinterpret_cast<u32x4*>(&vs[r * LS + c8]) = vr[i];
+      *reinterpret_cast<u32x4*>(&ks[buf * BUF + r * LS + c8]) = kr[i];
+      *reinterpret_cast<u32x4*>(&vs[buf * BUF + r * LS + c8]) = vr[i];
     }
   };
 
-  float m_run = kNegInf, l_run = 0.f;
-  f32x4 acc[ND];
+  float m_run[CG], l_run[CG];
+  f32x4 acc[CG][ND];
 #pragma unroll
-  for (int nd = 0; nd < ND; ++nd) acc[nd] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-  const int ntiles = (kmax + KT - 1) / KT;
-  fetch(0);
-  for (int kt = 0; kt < ntiles; ++kt) {
-    __syncthreads();  // every wavefront is done reading the previous tile
-    stash();
-    __syncthreads();
-    if (kt + 1 < ntiles) fetch(kt + 1);
-
-    // Scores of the tile: lane (row, grp) holds keys 16 s + 4 grp + r of column `row`.
-    float xs[NS][4];
-    float mloc = kNegInf;
+  for (int cg = 0; cg < CG; ++cg) {
+    m_run[cg] = kNegInf;
+    l_run[cg] = 0.f;
 #pragma unroll
-    for (int s = 0; s < NS; ++s) {
-      const int kb = kt * KT + s * 16;
-      if (kb < kmax) {  // workgroup-uniform
-        const f16* kp = ks + (s * 16 + row) * LS + grp * 8;
-        f32x4 sc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int c = 0; c < NC; ++c)
-          sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(*reinterpret_cast<const f16x8*>(kp + 32 * c),
-                                                      qf[c], sc, 0, 0, 0);
-        if (kb + 15 <= pmin) {  // every column sees the whole sub-tile
-#pragma unroll
-          for (int r = 0; r < 4; ++r) xs[s][r] = sc[r] * a.scale_log2;
-        } else {
-#pragma unroll
-          for (int r = 0; r < 4; ++r)
-            xs[s][r] = kb + grp * 4 + r <= pos_c ? sc[r] * a.scale_log2 : kNegInf;
-        }
-#pragma unroll
-        for (int r = 0; r < 4; ++r) mloc = fmaxf(mloc, xs[s][r]);
-      } else {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) xs[s][r] = kNegInf;
-      }
-    }
-    // Key 0 is in the first tile and visible to every column, so m_run is
-    // finite from the first tile on and no exp2 sees -inf - -inf.
-    mloc = fmaxf(mloc, __shfl_xor(mloc, 16));
-    mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
-    const float m_new = fmaxf(m_run, mloc);
-    const float alpha = fast_exp2(m_run - m_new);
-    l_run *= alpha;
-#pragma unroll
-    for (int nd = 0; nd < ND; ++nd) acc[nd] *= alpha;
-    m_run = m_new;
-
-#pragma unroll
-    for (int s = 0; s < NS; ++s) {
-      const int kb = kt * KT + s * 16;
-      if (kb < kmax) {
-        // P^T as the B operand: the score layout already is (column `row`,
-        // keys 4 grp + r). fp16 high part plus fp16 remainder keeps ~22 bits.
-        f16x4 ph, pl;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float pr = fast_exp2(xs[s][r] - m_run);
-          l_run += pr;
-          const f16 hi = (f16)pr;
-          ph[r] = hi;
-          pl[r] = (f16)(pr - (float)hi);
-        }
-        // V^T operand: lane (row, grp) needs V[4 grp + r][16 nd + row], r = 0..3,
-        // which one transposing read of key rows 4 grp .. 4 grp + 3 delivers.
-        const f16* vt = vs + (s * 16 + grp * 4 + (row >> 2)) * LS + (row & 3) * 4;
-#pragma unroll
-        for (int nd = 0; nd < ND; ++nd) {
-          const f16x4 av = lds_read_tr16(vt + nd * 16);
-          acc[nd] = __builtin_amdgcn_mfma_f32_16x16x16f16(av, ph, acc[nd], 0, 0, 0);
-          acc[nd] = __builtin_amdgcn_mfma_f32_16x16x16f16(av, pl, acc[nd], 0, 0, 0);
-        }
-      }
-    }
+    for (int nd = 0; nd < ND; ++nd) acc[cg][nd] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
 
-  // Denominator: each lane summed its own four keys per sub-tile.
-  float l = l_run;
-  l += __shfl_xor(l, 16);
-  l += __shfl_xor(l, 32);
-  if (col_ok) {
-    const float inv = pos >= 0 ? 1.f / l : 0.f;
+  // Two LDS buffers: tile kt is read from buffer kt % 2 while tile kt + 1 is
+  // written to the other, so each tile needs one barrier.
+  const int ntiles = (kmax + KT - 1) / KT;
+  fetch_ids(0);
+  fetch_kv(0);
+  fetch_ids(1);
+  stash(0);
+  __syncthreads();
+  for (int kt = 0; kt < ntiles; ++kt) {
+    const bool more = kt + 1 < ntiles;
+    if (more) {
+      fetch_kv(kt + 1);
+      fetch_ids(kt + 2);
+    }
+    const f16* kt_lds = ks + (kt & 1) * BUF;
+    const f16* vt_lds = vs + (kt & 1) * BUF;
+
+    // Raw scores of the whole tile, without branches: lane (row, grp) holds
+    // keys 16 s + 4 grp + r of its column in each group. Rows past the last
+    // key are zeros in LDS; the mask below removes them with the causal cut.
+    f32x4 sc[CG][NS];
 #pragma unroll
-    for (int nd = 0; nd < ND; ++nd) {
-      f16x4 o;
+    for (int s = 0; s < NS; ++s) {
+      f16x8 kf[NC];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) o[r] = (f16)(acc[nd][r] * inv);
-      *reinterpret_cast<f16x4*>(op + nd * 16) = o;
+      for (int c = 0; c < NC; ++c)
+        kf[c] = *reinterpret_cast<const f16x8*>(kt_lds + (s * 16 + row) * LS + grp * 8 + 32 * c);
+#pragma unroll
+      for (int cg = 0; cg < CG; ++cg) {
+        sc[cg][s] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int c = 0; c < NC; ++c)
+          sc[cg][s] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[c], qf[cg][c], sc[cg][s], 0, 0, 0);
+      }
+    }
+    if (kt * KT + KT - 1 > pmin) {  // workgroup-uniform: a tile crossing some column's position
+#pragma unroll
+      for (int cg = 0; cg < CG; ++cg)
+#pragma unroll
+        for (int s = 0; s < NS; ++s)
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            if (kt * KT + s * 16 + grp * 4 + r > pos_c[cg]) sc[cg][s][r] = kNegInf;
+    }
+    // Maxima in the exp2 domain (the scale is positive, so it commutes with
+    // the maximum). Key 0 is in the first tile and visible to every column,
+    // so the first tile raises every running maximum to a finite value.
+    float mloc[CG];
+    bool raise = false;
+#pragma unroll
+    for (int cg = 0; cg < CG; ++cg) {
+      float m = kNegInf;
+#pragma unroll
+      for (int s = 0; s < NS; ++s)
+        m = fmaxf(fmaxf(m, fmaxf(sc[cg][s][0], sc[cg][s][1])), fmaxf(sc[cg][s][2], sc[cg][s][3]));
+      m = fmaxf(m, __shfl_xor(m, 16));
+      m = fmaxf(m, __shfl_xor(m, 32));
+      mloc[cg] = m * a.scale_log2;
+      raise |= mloc[cg] > m_run[cg] + kLazy;
+    }
+    if (__builtin_amdgcn_ballot_w64(raise) != 0) {  // wavefront-uniform
+#pragma unroll
+      for (int cg = 0; cg < CG; ++cg) {
+        const float m_new = fmaxf(m_run[cg], mloc[cg]);
+        const float alpha = fast_exp2(m_run[cg] - m_new);
+        l_run[cg] *= alpha;
+#pragma unroll
+        for (int nd = 0; nd < ND; ++nd) acc[cg][nd] *= alpha;
+        m_run[cg] = m_new;
+      }
+    }
+
+    // O^T += V^T P^T over pairs of sub-tiles, 32 keys per MFMA: operand index
+    // k = 8 grp + i stands for key 16 s0 + 4 grp + i (i < 4) or 16 s1 + 4 grp
+    // + i - 4, in both the V^T and the P^T operand. Denominators sum the same
+    // fp16-rounded probabilities the products use.
+#pragma unroll
+    for (int sp = 0; sp < NS / 2; ++sp) {
+      const int s0 = 2 * sp, s1 = 2 * sp + 1;
+      f16x8 pb[CG];
+#pragma unroll
+      for (int cg = 0; cg < CG; ++cg) {
+        const float nm = -m_run[cg];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          pb[cg][r] = (f16)fast_exp2(__builtin_fmaf(sc[cg][s0][r], a.scale_log2, nm));
+          pb[cg][4 + r] = (f16)fast_exp2(__builtin_fmaf(sc[cg][s1][r], a.scale_log2, nm));
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          l_run[cg] = __builtin_amdgcn_fdot2(f16x2{pb[cg][2 * i], pb[cg][2 * i + 1]},
+                                             f16x2{(f16)1.f, (f16)1.f}, l_run[cg], false);
+      }
+      // V^T operand: lane (row, grp) needs V[16 s + 4 grp + r][16 nd + row],
+      // r = 0..3, which one transposing read of four key rows delivers.
+      const f16* v0 = vt_lds + (s0 * 16 + grp * 4 + (row >> 2)) * LS + (row & 3) * 4;
+      const f16* v1 = v0 + 16 * LS;
+#pragma unroll
+      for (int nd = 0; nd < ND; ++nd) {
+        const f16x4 a0 = lds_read_tr16(v0 + nd * 16);
+        const f16x4 a1 = lds_read_tr16(v1 + nd * 16);
+        const f16x8 av = {a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
+#pragma unroll
+        for (int cg = 0; cg < CG; ++cg)
+          acc[cg][nd] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, pb[cg], acc[cg][nd], 0, 0, 0);
+      }
+    }
+
+    if (more) stash((kt + 1) & 1);
+    __syncthreads();
+  }
+
+  // Denominators: each lane summed its own keys.
+#pragma unroll
+  for (int cg = 0; cg < CG; ++cg) {
+    float l = l_run[cg];
+    l += __shfl_xor(l, 16);
+    l += __shfl_xor(l, 32);
+    if (col_ok[cg]) {
+      const float inv = pos[cg] >= 0 ? 1.f / l : 0.f;
+#pragma unroll
+      for (int nd = 0; nd < ND; ++nd) {
+        f16x4 o;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) o[r] = (f16)(acc[cg][nd][r] * inv);
+        *reinterpret_cast<f16x4*>(op[cg] + nd * 16) = o;
+      }
     }
   }
 }
@@ -232,7 +298,11 @@ __global__ __launch_bounds__(256) void prefill_attn_kernel(PrefillAttnArgs a) {
 template <int D>
 static hipError_t launch_prefill_d(const PrefillAttnArgs& a, hipStream_t s) {
   const int64_t grid = (int64_t)a.col_blocks * a.num_seqs * a.hkv;
-  hipLaunchKernelGGL(prefill_attn_kernel<D>, dim3((unsigned)grid), dim3(256), 0, s, a);
+  constexpr int CG = prefill_col_groups(D);
+  if (a.bs == 16)
+    hipLaunchKernelGGL((prefill_attn_kernel<D, 16, CG>), dim3((unsigned)grid), dim3(256), 0, s, a);
+  else
+    hipLaunchKernelGGL((prefill_attn_kernel<D, 0, CG>), dim3((unsigned)grid), dim3(256), 0, s, a);
   return hipGetLastError();
 }
 
