@@ -50,6 +50,8 @@ def parse_args():
                    help="approximate CPU time budget of the oracle baseline sample")
     p.add_argument("--no-decode", action="store_true",
                    help="skip the decode-step tokens/sec measurement")
+    p.add_argument("--no-prefill", action="store_true",
+                   help="skip the prefix-prefill attention measurement")
     p.add_argument("--decode-batch", type=int, default=128)
     p.add_argument("--decode-steps", type=int, default=128)
     return p.parse_args()
@@ -125,6 +127,58 @@ def decode_benchmark(dev, seed, batch, steps):
         "prefill_s": round(prefill_s, 3),
         "model": "Qwen2.5-0.5B architecture, random init N(0, 0.02), fp16, untied lm_head",
         "prompt_lens": "U[64, 1024], random token ids",
+    }
+
+
+MFMA_F16_PEAK_TFLOPS = 2500.0
+
+
+def prefill_benchmark(dev, seed, iters=30, warmup=5):
+    """Paged prefill attention of prompt suffixes over cached prefix blocks.
+
+    8 sequences, each 2048 cached tokens plus 512 new ones, Qwen2.5-0.5B heads
+    (14 q / 2 kv, head_dim 64), block 16, shuffled physical blocks. The kernel
+    is MFMA work: causal FLOPs = 4 * head_dim * q_heads * (keys seen, summed
+    over the new tokens), priced against the dense fp16 MFMA peak.
+    """
+    import torch
+
+    from engine.kernels.paged_attention import paged_attention_prefill
+
+    B, cached, new, hq, hkv, d, bs = 8, 2048, 512, 14, 2, 64, 16
+    L = cached + new
+    nb = (L + bs - 1) // bs
+    g = torch.Generator(device=dev).manual_seed(seed + 11)
+    pool = B * nb + 16
+    kc = torch.randn(pool, bs, hkv, d, generator=g, device=dev).half()
+    vc = torch.randn(pool, bs, hkv, d, generator=g, device=dev).half()
+    perm = torch.randperm(pool, generator=g, device=dev)[:B * nb].to(torch.int32)
+    bt = perm.view(B, nb).contiguous()
+    lens = torch.full((B,), L, dtype=torch.int32, device=dev)
+    qsl = (torch.arange(B + 1, device=dev) * new).to(torch.int32)
+    q = torch.randn(B * new, hq, d, generator=g, device=dev).half()
+    for _ in range(warmup):
+        paged_attention_prefill(q, kc, vc, bt, lens, qsl, new, d ** -0.5)
+    torch.cuda.synchronize()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(iters)]
+    for a, b in ev:
+        a.record()
+        paged_attention_prefill(q, kc, vc, bt, lens, qsl, new, d ** -0.5)
+        b.record()
+    torch.cuda.synchronize()
+    us = statistics.fmean(a.elapsed_time(b) for a, b in ev) * 1e3
+    keys_seen = B * sum(cached + i + 1 for i in range(new))
+    flops = 4.0 * d * hq * keys_seen
+    tflops = flops / (us * 1e-6) / 1e12
+    return {
+        "config": {"workload": "prefix_prefill", "num_seqs": B, "cached_tokens": cached,
+                   "new_tokens": new, "num_q_heads": hq, "num_kv_heads": hkv, "head_dim": d,
+                   "block_size": bs},
+        "attention_us_mean": round(us, 2),
+        "flops": flops,
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 1), "peak": MFMA_F16_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(tflops / MFMA_F16_PEAK_TFLOPS, 4)},
     }
 
 
@@ -319,6 +373,8 @@ def main():
     result["copy_ceiling_gbps"] = copy_ceiling(dev)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(base, args.cpu_seconds)
+    if not args.no_prefill:
+        result["prefix_prefill"] = prefill_benchmark(dev, args.seed)
     if not args.no_decode:
         del copies, base
         torch.cuda.empty_cache()

@@ -43,9 +43,11 @@ HIPCC_FLAGS = [
 
 # Extra flags per source file. The prefill attention kernel rescales its MFMA
 # accumulators with vector ops; in the accumulator-register form every rescale
-# copies them out and back, so its MFMAs use the VGPR form.
+# copies them out and back, so its MFMAs use the VGPR form. Its score maxima
+# would otherwise quiet possible signalling NaNs with an extra v_max per value
+# (-fno-honor-nans; infinities, which the masking uses, keep their meaning).
 FILE_FLAGS = {
-    "pa_prefill.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+    "pa_prefill.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1", "-fno-honor-nans"],
 }
 
 

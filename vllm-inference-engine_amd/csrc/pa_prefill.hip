@@ -7,19 +7,23 @@
 //
 // Work split. The (token, query head) pairs of one sequence and one kv head
 // form a list of n * g columns, token-major. A workgroup of four wavefronts
-// takes 64 consecutive columns (16 per wavefront), so the K/V rows it stages
-// serve all g query heads of the kv head at once. Workgroups with the latest
-// columns see the most keys; they are numbered first so the longest run
-// starts first.
+// takes 128 consecutive columns (two groups of 16 per wavefront; 64 columns,
+// one group, at head_dim 256), so the K/V rows it stages serve all g query
+// heads of the kv head at once and each K or V operand read from LDS feeds
+// two MFMAs. Workgroups with the latest columns see the most keys; they are
+// numbered first so the longest runs start first.
 //
-// Per 64-key tile the workgroup loads K and V rows (16-byte loads, block id
-// per row from the table) into LDS, one tile ahead in registers. Each
-// wavefront computes S^T = K Q^T on MFMA (16 keys x 16 columns per
-// instruction, K read in the operand layout, Q kept in registers), masks keys
-// past each column's position, updates its online softmax in the exp2 domain
-// and accumulates O^T += V^T P^T on MFMA with V^T read transposed from LDS --
-// the operand layouts of the decode kernel, with columns that are (token,
-// head) pairs instead of the heads of one token.
+// Per key tile (128 keys up to head_dim 64, else 64) the workgroup loads K
+// and V rows (16-byte loads, block id per row from the table, fetched a tile
+// earlier) into registers one tile ahead, and stores them into two LDS
+// buffers used alternately, one barrier per tile. Each wavefront computes
+// S^T = K Q^T on MFMA (16 keys x 16 columns per instruction, K read in the
+// operand layout, Q kept in registers), masks keys past each column's
+// position (only on tiles that cross one), keeps an online softmax in the
+// exp2 domain whose maximum is raised lazily, and accumulates O^T += V^T P^T
+// with fp16 probabilities on K=32 MFMAs, V^T read transposed from LDS -- the
+// operand layouts of the decode kernel, with columns that are (token, head)
+// pairs instead of the heads of one token.
 #include "pa_tiles.h"
 
 namespace pa {
@@ -30,7 +34,10 @@ template <int D, int BS, int CG>
 __global__ __launch_bounds__(256) void prefill_attn_kernel(PrefillAttnArgs a) {
   constexpr int NW = 4;
   constexpr int COLS = 16 * CG * NW;  // columns per workgroup
-  constexpr int KT = 64;              // keys per staged tile
+  // Keys per staged tile: 128 up to head_dim 64 (more work per barrier), 64
+  // above, where two 128-key K and V buffers would not leave LDS for a second
+  // workgroup.
+  constexpr int KT = D <= 64 ? 128 : 64;
   constexpr int NS = KT / 16;         // 16-key sub-tiles per tile
   constexpr int NC = D / 32;
   constexpr int ND = D / 16;
