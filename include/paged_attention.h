@@ -50,7 +50,7 @@ enum {
 
 /* ABI revision of this header; bumps whenever a signature or a workspace
  * contract changes (2: zero-initialised decode workspace; 3: pa_rope_kv_write_f16;
- * 4: pa_prefill_attention_f16). */
+ * 4: pa_prefill_attention_f16; 5: its workspace). */
 PA_API int pa_abi_version(void);
 
 /* Message of the last failed call on this thread ("" after a success). */
@@ -209,8 +209,19 @@ PA_API int pa_rope_kv_write_f16(const void* q, const int64_t q_strides[3], const
  * head h / (num_q_heads / num_kv_heads). max_query_len must be at least every
  * n_b (rows past it are not computed); rows with p < 0 are written as zeros;
  * rows outside every sequence's range are not written. scale must be positive
- * and finite. Needs no workspace.
+ * and finite.
+ *
+ * Workspace: when the column blocks of the launch are too few to fill the GPU,
+ * long key ranges are split over several workgroups, whose partial results
+ * meet in the workspace; pa_prefill_attention_workspace_bytes() gives its size
+ * (0: none needed). Like the decode workspace it starts with arrival counters
+ * that must be zero before the buffer's first use and that every call leaves
+ * zero; use one buffer per stream and lend it to nothing else.
  */
+PA_API size_t pa_prefill_attention_workspace_bytes(int num_seqs, int num_q_heads,
+                                                   int num_kv_heads, int head_dim,
+                                                   int block_size, int max_blocks_per_seq,
+                                                   int max_query_len);
 PA_API int pa_prefill_attention_f16(const void* q, const int64_t q_strides[3],
                                     const void* k_cache, const int64_t k_strides[4],
                                     const void* v_cache, const int64_t v_strides[4],
@@ -220,7 +231,7 @@ PA_API int pa_prefill_attention_f16(const void* q, const int64_t q_strides[3],
                                     int num_seqs, int num_tokens, int num_q_heads,
                                     int num_kv_heads, int head_dim, int block_size,
                                     int num_blocks, int max_blocks_per_seq, float scale,
-                                    void* stream);
+                                    void* workspace, size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -55,6 +55,16 @@ def test_workspace_sizes():
     assert lib.pa_decode_batched_workspace_bytes(2000, 14, 2, 64, 16, 32) == 0
     assert lib.pa_decode_v1_workspace_bytes(14, 2, 64, 16, 67) == 2 * 16 * 80 * 4
     assert lib.pa_decode_batched_workspace_bytes(8, 14, 2, 48, 16, 2048) == 0  # unsupported dim
+    # Prefill: one sequence, 512 new tokens of 2560 (7 x 512 / 128 = 28 column blocks x 2 kv
+    # heads = 56 workgroups, fewer than 3/4 of 2 x 256 slots): 20 key tiles of 128 split in 5
+    # pieces of 4; the fixed counter region (16384 ints), then 56 x 5 records of 128 columns
+    # x (64 + 2) floats.
+    assert lib.pa_prefill_attention_workspace_bytes(1, 14, 2, 64, 16, 160, 512) == \
+        16384 * 4 + 56 * 5 * 128 * 66 * 4
+    # 64 sequences give 3584 workgroups: no split, no workspace.
+    assert lib.pa_prefill_attention_workspace_bytes(64, 14, 2, 64, 16, 160, 512) == 0
+    # Short contexts (at most 4 key tiles) are never split.
+    assert lib.pa_prefill_attention_workspace_bytes(1, 14, 2, 64, 16, 32, 16) == 0
 
 
 def _strides(*vals):
@@ -98,7 +108,7 @@ def _prefill_call(lib, head_dim=64, nq=14, nkv=2, q=16, qstart=16, qstr=(896, 64
     return lib.pa_prefill_attention_f16(
         q, _strides(*qstr), 16, _strides(*kstr), 16, _strides(*kstr), 16, _strides(64, 1), 16,
         qstart, maxq, 16, _strides(896, 64, 1), 4, ntok, nq, nkv, head_dim, 16, 100, 64, scale,
-        None)
+        None, 0, None)
 
 
 def test_prefill_argument_errors():

@@ -14,6 +14,7 @@ import random
 import pytest
 import torch
 
+from engine.kernels import _native
 from engine.kernels.paged_attention import (
     paged_attention_decode_batched,
     paged_attention_prefill,
@@ -153,3 +154,54 @@ def test_query_rows_placed_by_query_start_loc(cuda_device):
     qsl = torch.tensor([2, 10], dtype=torch.int32, device=cuda_device)
     out = paged_attention_prefill(q, c["kd"], c["vd"], c["btd"], c["lensd"], qsl, 8, 0.125)
     assert max_err(out[2:10], oracle(c, 0.125)) <= TOL
+
+
+def test_single_sequence_long_prefix_split(cuda_device):
+    """One sequence (the reference prefills one at a time): its few column blocks are split
+    along the keys over several workgroups, merged in the kernel."""
+    c = build(14, 2, 64, 16, [8192], [1024], seed=18, device=cuda_device)
+    out = run(c, 0.125)
+    err = max_err(out, oracle(c, 0.125))
+    print(f"[prefill] single long max_err={err:.2e}", flush=True)
+    assert err <= TOL
+    for _ in range(2):
+        assert torch.equal(run(c, 0.125), out)
+
+
+def test_split_counters_return_to_zero(cuda_device):
+    c = build(28, 4, 128, 16, [3000, 10], [700, 10], seed=19, device=cuda_device)
+    run(c, 128 ** -0.5)
+    torch.cuda.synchronize()
+    stream = _native.stream_handle(cuda_device)
+    ws = _native._workspaces.get((cuda_device.index, stream, _native.WS_PREFILL))
+    assert ws is not None, "this launch should have split its key ranges"
+    lib = _native.load()
+    need = lib.pa_prefill_attention_workspace_bytes(2, 28, 4, 128, 16, c["btd"].shape[1], 700)
+    assert need > 0
+    # The fixed counter region at the start of the buffer (16384 ints) is all zero again.
+    assert torch.count_nonzero(ws[:16384 * 4]) == 0
+    assert max_err(run(c, 128 ** -0.5), oracle(c, 128 ** -0.5)) <= TOL
+
+
+def test_launches_of_different_sizes_share_the_scratch(cuda_device):
+    """Split launches of different sizes in a row reuse one scratch buffer: each finds its
+    counters at zero, whatever the previous launch left in its records."""
+    cases = [build(14, 2, 64, 16, [3000], [200], seed=22, device=cuda_device),
+             build(28, 4, 128, 16, [5000, 900], [1000, 3], seed=23, device=cuda_device),
+             build(14, 2, 64, 16, [2500, 2600], [64, 100], seed=24, device=cuda_device)]
+    want = [oracle(c, 0.125) for c in cases]
+    for _ in range(2):
+        for c, w in zip(cases, want):
+            assert max_err(run(c, 0.125), w) <= TOL
+
+
+def test_prefill_and_decode_interleaved_on_one_stream(cuda_device):
+    """Both kernels keep their own scratch; alternating them changes no result."""
+    c = build(14, 2, 64, 16, [2000, 600], [300, 1], seed=20, device=cuda_device)
+    d = build(14, 2, 64, 16, [4000, 37, 900], [1, 1, 1], seed=21, device=cuda_device)
+    p0 = run(c, 0.125)
+    d0 = paged_attention_decode_batched(d["qd"], d["kd"], d["vd"], d["btd"], d["lensd"], 0.125)
+    for _ in range(3):
+        assert torch.equal(run(c, 0.125), p0)
+        assert torch.equal(paged_attention_decode_batched(d["qd"], d["kd"], d["vd"], d["btd"],
+                                                          d["lensd"], 0.125), d0)

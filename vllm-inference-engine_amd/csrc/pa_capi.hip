@@ -169,13 +169,59 @@ static hipError_t launch_streamk_with(DecodeArgs& a, int num_seqs, int head_dim,
   return launch_decode_streamk(a, head_dim, s);
 }
 
+// ---- prefill attention: key-range split plan and workspace layout ----
+
+// Fewest key tiles a split of the prefill kernel takes.
+constexpr int kPrefillMinSplitTiles = 4;
+
+struct PrefillPlan {
+  int64_t col_blocks = 0, split_tiles = 1, max_splits = 1;
+  size_t counter_bytes = 0, ws_bytes = 0;
+};
+
+// Column blocks of `cols` (token, head) columns per (sequence, kv head). When
+// they fill less than three quarters of the GPU's resident workgroup slots,
+// each column block's key range is split into pieces of split_tiles key tiles
+// (at least kPrefillMinSplitTiles) so that about that many workgroups exist. The
+// workspace then holds the fixed counter region (kPfCounterBytes, one counter
+// per column block, zero between launches) and a record of (head_dim + 2) x
+// cols floats per split.
+static PrefillPlan prefill_plan(int num_seqs, int num_q_heads, int num_kv_heads, int head_dim,
+                                int block_size, int max_blocks, int max_query_len) {
+  PrefillPlan p;
+  const int g = num_q_heads / num_kv_heads;
+  const int cols = prefill_cols_per_wg(head_dim);
+  p.col_blocks = ((int64_t)max_query_len * g + cols - 1) / cols;
+  const int kt = prefill_key_tile(head_dim);
+  const int64_t max_tiles = ((int64_t)max_blocks * block_size + kt - 1) / kt;
+  const int64_t base = p.col_blocks * num_seqs * num_kv_heads;
+  // The kernel keeps two workgroups per CU resident (one at head_dim 256, for
+  // LDS); splitting pays only while the column blocks fill less than about
+  // three quarters of those slots.
+  const int64_t target = (int64_t)device_cus() * (head_dim <= 128 ? 2 : 1) * 3 / 4;
+  p.split_tiles = max_tiles < 1 ? 1 : max_tiles;
+  if (base > 0 && base < target && base <= kPfMaxCounters && max_tiles > kPrefillMinSplitTiles) {
+    const int64_t want = (target + base - 1) / base;
+    int64_t st = (max_tiles + want - 1) / want;
+    if (st < kPrefillMinSplitTiles) st = kPrefillMinSplitTiles;
+    p.split_tiles = st;
+    p.max_splits = (max_tiles + st - 1) / st;
+  }
+  if (p.max_splits > 1) {
+    p.counter_bytes = kPfCounterBytes;
+    p.ws_bytes = p.counter_bytes +
+                 (size_t)base * p.max_splits * cols * (head_dim + 2) * sizeof(float);
+  }
+  return p;
+}
+
 }  // namespace pa
 
 using namespace pa;
 
 extern "C" {
 
-int pa_abi_version(void) { return 4; }
+int pa_abi_version(void) { return 5; }
 
 const char* pa_last_error(void) { return g_error.c_str(); }
 
@@ -601,6 +647,17 @@ int pa_rope_kv_write_f16(const void* q, const int64_t q_strides[3], const void* 
   return finish_launch(launch_rope_kv_write(a, vec, (hipStream_t)stream));
 }
 
+size_t pa_prefill_attention_workspace_bytes(int num_seqs, int num_q_heads, int num_kv_heads,
+                                            int head_dim, int block_size,
+                                            int max_blocks_per_seq, int max_query_len) {
+  if (num_seqs <= 0 || num_kv_heads <= 0 || num_q_heads <= 0 || num_q_heads % num_kv_heads ||
+      block_size <= 0 || max_blocks_per_seq <= 0 || max_query_len <= 0 ||
+      !supported_head_dim(head_dim))
+    return 0;
+  return prefill_plan(num_seqs, num_q_heads, num_kv_heads, head_dim, block_size,
+                      max_blocks_per_seq, max_query_len).ws_bytes;
+}
+
 int pa_prefill_attention_f16(const void* q, const int64_t q_strides[3], const void* k_cache,
                              const int64_t k_strides[4], const void* v_cache,
                              const int64_t v_strides[4], const int32_t* block_tables,
@@ -608,7 +665,8 @@ int pa_prefill_attention_f16(const void* q, const int64_t q_strides[3], const vo
                              const int32_t* query_start_loc, int max_query_len, void* out,
                              const int64_t out_strides[3], int num_seqs, int num_tokens,
                              int num_q_heads, int num_kv_heads, int head_dim, int block_size,
-                             int num_blocks, int max_blocks_per_seq, float scale, void* stream) {
+                             int num_blocks, int max_blocks_per_seq, float scale,
+                             void* workspace, size_t workspace_bytes, void* stream) {
   clear_error();
   if (num_seqs < 0 || num_tokens < 0 || max_query_len < 0) {
     set_error("num_seqs, num_tokens and max_query_len must be >= 0");
@@ -638,12 +696,16 @@ int pa_prefill_attention_f16(const void* q, const int64_t q_strides[3], const vo
     return PA_ERR_ARG;
   }
   const int g = num_q_heads / num_kv_heads;
-  const int cols = prefill_cols_per_wg(head_dim);
-  const int64_t col_blocks = ((int64_t)max_query_len * g + cols - 1) / cols;
-  const int64_t grid = col_blocks * num_seqs * num_kv_heads;
-  if (grid > 0x7fffffff) {
+  const PrefillPlan plan = prefill_plan(num_seqs, num_q_heads, num_kv_heads, head_dim, block_size,
+                                        max_blocks_per_seq, max_query_len);
+  const int64_t grid = plan.col_blocks * plan.max_splits * num_seqs * num_kv_heads;
+  if (grid > 0x7fffffff || plan.col_blocks > 0x7fffffff) {
     set_error("%lld workgroups exceed the grid limit", (long long)grid);
     return PA_ERR_UNSUPPORTED;
+  }
+  if (plan.ws_bytes && (!workspace || workspace_bytes < plan.ws_bytes)) {
+    set_error("workspace of %zu bytes needed, %zu given", plan.ws_bytes, workspace_bytes);
+    return PA_ERR_WORKSPACE;
   }
   PrefillAttnArgs a{};
   a.q = (const f16*)q;
@@ -672,8 +734,12 @@ int pa_prefill_attention_f16(const void* q, const int64_t q_strides[3], const vo
   a.bs = block_size;
   a.num_blocks = num_blocks;
   a.max_blocks = max_blocks_per_seq;
-  a.col_blocks = (int)col_blocks;
+  a.col_blocks = (int)plan.col_blocks;
   a.scale_log2 = scale * kLog2e;
+  a.split_tiles = (int)plan.split_tiles;
+  a.max_splits = (int)plan.max_splits;
+  a.cnt = plan.ws_bytes ? (int*)workspace : nullptr;
+  a.recs = plan.ws_bytes ? (float*)((char*)workspace + plan.counter_bytes) : nullptr;
   return finish_launch(launch_prefill_attn(a, head_dim, (hipStream_t)stream));
 }
 

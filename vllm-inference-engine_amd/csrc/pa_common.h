@@ -144,6 +144,12 @@ struct PrefillAttnArgs {
   int num_seqs, num_tokens, hkv, g, bs, num_blocks, max_blocks;
   int col_blocks;  // column blocks per (sequence, kv head): ceil(max_query_len * g / columns)
   float scale_log2;
+  // Key-range split: a column block whose keys span more than split_tiles key
+  // tiles is processed by several workgroups (up to max_splits), which leave
+  // partial records; the last to finish merges them.
+  int split_tiles, max_splits;
+  int* cnt;     // per-column-block arrival counters, zero between launches
+  float* recs;  // [seq][kv head][column block][split] records of (D + 2) x columns floats
 };
 
 // Column groups of 16 (token, query head) columns each prefill wavefront
@@ -151,6 +157,15 @@ struct PrefillAttnArgs {
 // registers allow it, so each K and V operand read from LDS feeds two MFMAs.
 __host__ __device__ constexpr int prefill_col_groups(int D) { return D <= 128 ? 2 : 1; }
 __host__ __device__ constexpr int prefill_cols_per_wg(int D) { return 64 * prefill_col_groups(D); }
+// The prefill workspace starts with a fixed region of arrival counters, one per
+// column block of a split launch, so that the counters of every launch sit at
+// the same place whatever its size and never overlap an earlier launch's
+// records (launches that split have fewer column blocks than this).
+constexpr int kPfMaxCounters = 16384;
+constexpr size_t kPfCounterBytes = (size_t)kPfMaxCounters * sizeof(int);
+// Keys per staged prefill tile: 128 up to head_dim 64, 64 above (two K and V
+// buffers of 128 keys would leave no LDS for a second workgroup).
+__host__ __device__ constexpr int prefill_key_tile(int D) { return D <= 64 ? 128 : 64; }
 
 // Launchers (defined next to their kernels).
 hipError_t launch_decode_split(const DecodeArgs& a, int D, int num_seqs, hipStream_t s);

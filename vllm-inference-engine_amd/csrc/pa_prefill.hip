@@ -34,10 +34,7 @@ template <int D, int BS, int CG>
 __global__ __launch_bounds__(256) void prefill_attn_kernel(PrefillAttnArgs a) {
   constexpr int NW = 4;
   constexpr int COLS = 16 * CG * NW;  // columns per workgroup
-  // Keys per staged tile: 128 up to head_dim 64 (more work per barrier), 64
-  // above, where two 128-key K and V buffers would not leave LDS for a second
-  // workgroup.
-  constexpr int KT = D <= 64 ? 128 : 64;
+  constexpr int KT = prefill_key_tile(D);  // keys per staged tile
   constexpr int NS = KT / 16;         // 16-key sub-tiles per tile
   constexpr int NC = D / 32;
   constexpr int ND = D / 16;
@@ -61,9 +58,14 @@ __global__ __launch_bounds__(256) void prefill_attn_kernel(PrefillAttnArgs a) {
   const int row = lane & 15;
   const int grp = lane >> 4;
 
+  // Workgroup -> (column block, key split, sequence, kv head); the column
+  // blocks with the most keys come first.
   const int per_cb = a.num_seqs * a.hkv;
-  const int cb = a.col_blocks - 1 - (int)(blockIdx.x / per_cb);
-  const int rest = (int)(blockIdx.x % per_cb);
+  const int cbi = (int)(blockIdx.x / (per_cb * a.max_splits));
+  const int rem = (int)(blockIdx.x - (unsigned)cbi * per_cb * a.max_splits);
+  const int split = rem / per_cb;
+  const int rest = rem - split * per_cb;
+  const int cb = a.col_blocks - 1 - cbi;
   const int b = rest / a.hkv;
   const int h = rest - b * a.hkv;
 
@@ -82,6 +84,11 @@ __global__ __launch_bounds__(256) void prefill_attn_kernel(PrefillAttnArgs a) {
   const int pos0 = L - qlen;                // position of the first new token
   const int kmax = pos0 + clast / a.g + 1;  // keys [0, kmax) are read
   const int pmin = pos0 + cfirst / a.g;     // every column sees keys [0, pmin]
+  const int ntiles = kmax > 0 ? (kmax + KT - 1) / KT : 0;
+  const int nsplit = ntiles > a.split_tiles ? (ntiles + a.split_tiles - 1) / a.split_tiles : 1;
+  if (split >= nsplit) return;
+  const int t0 = split * a.split_tiles;                       // this workgroup's key tiles
+  const int t1 = min(t0 + a.split_tiles, ntiles);             // [t0, t1)
 
   // This lane's columns (one per column group); columns past the list compute
   // as the last valid one and are not stored.
@@ -173,14 +180,13 @@ __global__ __launch_bounds__(256) void prefill_attn_kernel(PrefillAttnArgs a) {
 
   // Two LDS buffers: tile kt is read from buffer kt % 2 while tile kt + 1 is
   // written to the other, so each tile needs one barrier.
-  const int ntiles = (kmax + KT - 1) / KT;
-  fetch_ids(0);
-  fetch_kv(0);
-  fetch_ids(1);
-  stash(0);
+  fetch_ids(t0);
+  fetch_kv(t0);
+  fetch_ids(t0 + 1);
+  stash(t0 & 1);
   __syncthreads();
-  for (int kt = 0; kt < ntiles; ++kt) {
-    const bool more = kt + 1 < ntiles;
+  for (int kt = t0; kt < t1; ++kt) {
+    const bool more = kt + 1 < t1;
     if (more) {
       fetch_kv(kt + 1);
       fetch_ids(kt + 2);
@@ -216,8 +222,9 @@ __global__ __launch_bounds__(256) void prefill_attn_kernel(PrefillAttnArgs a) {
             if (kt * KT + s * 16 + grp * 4 + r > pos_c[cg]) sc[cg][s][r] = kNegInf;
     }
     // Maxima in the exp2 domain (the scale is positive, so it commutes with
-    // the maximum). Key 0 is in the first tile and visible to every column,
-    // so the first tile raises every running maximum to a finite value.
+    // the maximum). A column whose keys in this split are all masked so far
+    // keeps -inf (only possible in a split after the first, since key 0 is
+    // visible to every column).
     float mloc[CG];
     bool raise = false;
 #pragma unroll
@@ -235,7 +242,9 @@ __global__ __launch_bounds__(256) void prefill_attn_kernel(PrefillAttnArgs a) {
 #pragma unroll
       for (int cg = 0; cg < CG; ++cg) {
         const float m_new = fmaxf(m_run[cg], mloc[cg]);
-        const float alpha = fast_exp2(m_run[cg] - m_new);
+        // A column with no visible key yet (only in a split after the first)
+        // stays at -inf, and -inf - -inf would make its alpha NaN.
+        const float alpha = m_new == kNegInf ? 1.f : fast_exp2(m_run[cg] - m_new);
         l_run[cg] *= alpha;
 #pragma unroll
         for (int nd = 0; nd < ND; ++nd) acc[cg][nd] *= alpha;
@@ -253,7 +262,9 @@ __global__ __launch_bounds__(256) void prefill_attn_kernel(PrefillAttnArgs a) {
       f16x8 pb[CG];
 #pragma unroll
       for (int cg = 0; cg < CG; ++cg) {
-        const float nm = -m_run[cg];
+        // With no visible key yet every score is -inf; any finite offset then
+        // gives p = 0 (-inf - -inf would be NaN).
+        const float nm = m_run[cg] == kNegInf ? 0.f : -m_run[cg];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           pb[cg][r] = (f16)fast_exp2(__builtin_fmaf(sc[cg][s0][r], a.scale_log2, nm));
@@ -284,27 +295,115 @@ __global__ __launch_bounds__(256) void prefill_attn_kernel(PrefillAttnArgs a) {
   }
 
   // Denominators: each lane summed its own keys.
+  float lsum[CG];
 #pragma unroll
   for (int cg = 0; cg < CG; ++cg) {
     float l = l_run[cg];
     l += __shfl_xor(l, 16);
     l += __shfl_xor(l, 32);
-    if (col_ok[cg]) {
-      const float inv = pos[cg] >= 0 ? 1.f / l : 0.f;
+    lsum[cg] = l;
+  }
+  if (nsplit == 1) {
 #pragma unroll
-      for (int nd = 0; nd < ND; ++nd) {
-        f16x4 o;
+    for (int cg = 0; cg < CG; ++cg) {
+      if (col_ok[cg]) {
+        const float inv = pos[cg] >= 0 ? 1.f / lsum[cg] : 0.f;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) o[r] = (f16)(acc[cg][nd][r] * inv);
-        *reinterpret_cast<f16x4*>(op[cg] + nd * 16) = o;
+        for (int nd = 0; nd < ND; ++nd) {
+          f16x4 o;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) o[r] = (f16)(acc[cg][nd][r] * inv);
+          *reinterpret_cast<f16x4*>(op[cg] + nd * 16) = o;
+        }
+      }
+    }
+    return;
+  }
+
+  // Several splits: leave this split's record -- per column the running
+  // maximum, the denominator and the unnormalised accumulators -- with
+  // device-coherent stores (the splits run on any XCD), then count the
+  // arrival. The split completing the count merges every record in split
+  // order and resets the counter for the next launch.
+  constexpr int REC = COLS * (D + 2);  // floats of one record: maxima, denominators, accumulators
+  const int64_t blk = ((int64_t)b * a.hkv + h) * a.col_blocks + cb;
+  const auto rr = tile_rsrc(a.recs + blk * a.max_splits * REC, nsplit * REC * 4);
+  {
+    const int rb = split * REC * 4;  // byte offset of this split's record
+#pragma unroll
+    for (int cg = 0; cg < CG; ++cg) {
+      const int cl = (wave * CG + cg) * 16 + row;
+      if (grp == 0) {
+        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, m_run[cg]), rr,
+                                              rb + cl * 4, 0, 16);
+        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, lsum[cg]), rr,
+                                              rb + (COLS + cl) * 4, 0, 16);
+      }
+#pragma unroll
+      for (int nd = 0; nd < ND; ++nd)
+        store_coherent16(rr, rb + (2 * COLS + cl * D + nd * 16 + grp * 4) * 4, acc[cg][nd]);
+    }
+  }
+  __shared__ int s_last;
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (tid == 0)
+    s_last = __hip_atomic_fetch_add(a.cnt + blk, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+             nsplit - 1;
+  __syncthreads();
+  if (!s_last) return;
+
+  // Merge: TPC threads per column, each DPT consecutive values of head_dim,
+  // read as 16-byte device-coherent loads (all of a split's issued together).
+  constexpr int TPC = 64 * NW / COLS;
+  constexpr int DPT = D / TPC;
+  {
+    const int cl = tid / TPC;
+    const int d0 = (tid - cl * TPC) * DPT;
+    const int col = cfirst + cl;
+    if (col < ncols) {
+      const int tt = col / a.g;
+      const int jj = col - tt * a.g;
+      f16* o = a.out + (int64_t)(q0 + tt) * a.o_st + (int64_t)(h * a.g + jj) * a.o_sh + d0;
+      f32x4 v[DPT / 4];
+#pragma unroll
+      for (int i = 0; i < DPT / 4; ++i) v[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+      float L = 0.f;
+      if (pos0 + tt >= 0) {
+        float M = kNegInf;
+#pragma unroll 8
+        for (int sp = 0; sp < nsplit; ++sp) M = fmaxf(M, load_coherent4(rr, (sp * REC + cl) * 4));
+        for (int sp = 0; sp < nsplit; ++sp) {
+          const int rb = sp * REC * 4;
+          f32x4 part[DPT / 4];
+#pragma unroll
+          for (int i = 0; i < DPT / 4; ++i)
+            part[i] = load_coherent16(rr, rb + (2 * COLS + cl * D + d0 + 4 * i) * 4);
+          const float m = load_coherent4(rr, rb + cl * 4);
+          const float l = load_coherent4(rr, rb + (COLS + cl) * 4);
+          // A split that saw no key of this column has m = -inf and l = 0.
+          const float w = m == kNegInf ? 0.f : fast_exp2(m - M);
+          L += l * w;
+#pragma unroll
+          for (int i = 0; i < DPT / 4; ++i) v[i] += w * part[i];
+        }
+        L = 1.f / L;
+      }
+#pragma unroll
+      for (int i = 0; i < DPT / 4; ++i) {
+        f16x4 h4;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) h4[r] = (f16)(v[i][r] * L);
+        *reinterpret_cast<f16x4*>(o + 4 * i) = h4;
       }
     }
   }
+  if (tid == 0) __hip_atomic_store(a.cnt + blk, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 template <int D>
 static hipError_t launch_prefill_d(const PrefillAttnArgs& a, hipStream_t s) {
-  const int64_t grid = (int64_t)a.col_blocks * a.num_seqs * a.hkv;
+  const int64_t grid = (int64_t)a.col_blocks * a.max_splits * a.num_seqs * a.hkv;
   constexpr int CG = prefill_col_groups(D);
   if (a.bs == 16)
     hipLaunchKernelGGL((prefill_attn_kernel<D, 16, CG>), dim3((unsigned)grid), dim3(256), 0, s, a);

@@ -71,6 +71,20 @@ __device__ inline float load_coherent(const float* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// 16-byte forms of the same device-coherent accesses, through a buffer
+// resource (cache policy sc1, the bit the agent-scope stores and loads above
+// carry). Unlike atomic loads, the compiler issues many of these before
+// waiting, so reading a record costs one memory round trip.
+__device__ inline void store_coherent16(__amdgpu_buffer_rsrc_t r, int byte_off, f32x4 v) {
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, byte_off, 0, 16);
+}
+__device__ inline f32x4 load_coherent16(__amdgpu_buffer_rsrc_t r, int byte_off) {
+  return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 16));
+}
+__device__ inline float load_coherent4(__amdgpu_buffer_rsrc_t r, int byte_off) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, byte_off, 0, 16));
+}
+
 // Read of a table entry at a wavefront-uniform address through the scalar
 // data cache (s_load): the block tables and lengths are never written by
 // these kernels, and scalar loads are counted apart from the vector loads, so

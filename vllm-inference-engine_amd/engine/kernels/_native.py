@@ -17,7 +17,7 @@ import torch  # noqa: F401  (must be loaded before the HIP library, see above)
 
 LIB_NAME = "libpa_gfx950.so"
 LIB_PATH = Path(__file__).with_name(LIB_NAME)
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 PA_OK = 0
 PA_ERR_ARG = 1
@@ -60,7 +60,8 @@ SIGNATURES: dict[str, tuple] = {
         _i32, _i32, _i32, _i32, _i32, _i32, _i32, _vp]),
     "pa_prefill_attention_f16": (_i32, [
         _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _vp, _i32, _vp, _i64p,
-        _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _f32, _vp]),
+        _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _f32, _vp, _sz, _vp]),
+    "pa_prefill_attention_workspace_bytes": (_sz, [_i32, _i32, _i32, _i32, _i32, _i32, _i32]),
 }
 
 _lib = None
@@ -131,6 +132,9 @@ _workspaces: dict[tuple, torch.Tensor] = {}
 # pa_decode_v1_f16 (score rows, no zero requirement).
 WS_DECODE = "decode"
 WS_SCORES = "scores"
+# "prefill" serves pa_prefill_attention_f16: its counters follow the same
+# zero-between-calls contract as the decode ones, with another layout.
+WS_PREFILL = "prefill"
 
 
 def workspace(nbytes: int, device: torch.device, stream: int, kind: str = WS_DECODE) -> int | None:

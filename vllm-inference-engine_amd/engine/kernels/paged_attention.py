@@ -145,7 +145,9 @@ def paged_attention_prefill(
     position seq_lens[b] - n_b + i and sees pool positions 0 .. that position.
     max_query_len (a host int, at least every n_b) sizes the grid, so the
     call never reads device memory on the host. Asynchronous on the current
-    stream; no workspace.
+    stream. When the launch has too few column blocks to fill the GPU, long
+    key ranges are split over several workgroups that merge through a
+    per-stream scratch buffer (zero-filled once, like the decode one).
     """
     assert q.is_cuda and k_cache.is_cuda and v_cache.is_cuda
     assert block_tables.is_cuda and seq_lens.is_cuda and query_start_loc.is_cuda
@@ -170,6 +172,13 @@ def paged_attention_prefill(
         return out
     lib = _native.load()
     dev = q.device
+    max_blocks = block_tables.shape[1]
+    key = ("prefill", num_seqs, num_q_heads, num_kv_heads, head_dim, block_size, max_blocks,
+           int(max_query_len), dev.index)
+    ws_bytes = _ws_sizes.get(key)
+    if ws_bytes is None:
+        ws_bytes = _ws_sizes[key] = lib.pa_prefill_attention_workspace_bytes(*key[1:8])
+    stream = _native.stream_handle(dev)
     with _on_device(dev):
         status = lib.pa_prefill_attention_f16(
             q.data_ptr(), _native.strides_of(q),
@@ -179,7 +188,8 @@ def paged_attention_prefill(
             seq_lens.data_ptr(), query_start_loc.data_ptr(), int(max_query_len),
             out.data_ptr(), _native.strides_of(out),
             num_seqs, num_tokens, num_q_heads, num_kv_heads, head_dim, block_size, num_blocks,
-            block_tables.shape[1], float(scale), _native.stream_handle(dev))
+            max_blocks, float(scale), _native.workspace(ws_bytes, dev, stream, _native.WS_PREFILL),
+            ws_bytes, stream)
     _native.check(status, "pa_prefill_attention_f16")
     return out
 
