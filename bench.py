@@ -133,19 +133,19 @@ def decode_benchmark(dev, seed, batch, steps):
 MFMA_F16_PEAK_TFLOPS = 2500.0
 
 
-def prefill_benchmark(dev, seed, iters=30, warmup=5):
+def prefill_benchmark(dev, seed, B=8, cached=2048, new=512, iters=30, warmup=5):
     """Paged prefill attention of prompt suffixes over cached prefix blocks.
 
-    8 sequences, each 2048 cached tokens plus 512 new ones, Qwen2.5-0.5B heads
-    (14 q / 2 kv, head_dim 64), block 16, shuffled physical blocks. The kernel
-    is MFMA work: causal FLOPs = 4 * head_dim * q_heads * (keys seen, summed
-    over the new tokens), priced against the dense fp16 MFMA peak.
+    B sequences, each `cached` cached tokens plus `new` new ones, Qwen2.5-0.5B
+    heads (14 q / 2 kv, head_dim 64), block 16, shuffled physical blocks. The
+    kernel is MFMA work: causal FLOPs = 4 * head_dim * q_heads * (keys seen,
+    summed over the new tokens), priced against the dense fp16 MFMA peak.
     """
     import torch
 
     from engine.kernels.paged_attention import paged_attention_prefill
 
-    B, cached, new, hq, hkv, d, bs = 8, 2048, 512, 14, 2, 64, 16
+    hq, hkv, d, bs = 14, 2, 64, 16
     L = cached + new
     nb = (L + bs - 1) // bs
     g = torch.Generator(device=dev).manual_seed(seed + 11)
@@ -374,7 +374,11 @@ def main():
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(base, args.cpu_seconds)
     if not args.no_prefill:
+        # A batch of prompt suffixes, and one long prompt the way the reference
+        # prefills (one sequence at a time; its key ranges are split).
         result["prefix_prefill"] = prefill_benchmark(dev, args.seed)
+        result["prefix_prefill_single"] = prefill_benchmark(dev, args.seed, B=1, cached=8192,
+                                                            new=1024)
     if not args.no_decode:
         del copies, base
         torch.cuda.empty_cache()
