@@ -354,9 +354,12 @@ __global__ __launch_bounds__(256) void prefill_attn_kernel(PrefillAttnArgs a) {
   if (!s_last) return;
 
   // Merge: TPC threads per column, each DPT consecutive values of head_dim,
-  // read as 16-byte device-coherent loads (all of a split's issued together).
+  // read as 16-byte device-coherent loads. Records are combined MS at a time
+  // (as many as registers allow) with a running maximum -- log-sum-exp in
+  // split order -- so a merge costs about one memory round trip per MS splits.
   constexpr int TPC = 64 * NW / COLS;
   constexpr int DPT = D / TPC;
+  constexpr int MS = DPT <= 32 ? 2 : 1;
   {
     const int cl = tid / TPC;
     const int d0 = (tid - cl * TPC) * DPT;
@@ -370,22 +373,37 @@ __global__ __launch_bounds__(256) void prefill_attn_kernel(PrefillAttnArgs a) {
       for (int i = 0; i < DPT / 4; ++i) v[i] = f32x4{0.f, 0.f, 0.f, 0.f};
       float L = 0.f;
       if (pos0 + tt >= 0) {
-        float M = kNegInf;
-#pragma unroll 8
-        for (int sp = 0; sp < nsplit; ++sp) M = fmaxf(M, load_coherent4(rr, (sp * REC + cl) * 4));
-        for (int sp = 0; sp < nsplit; ++sp) {
-          const int rb = sp * REC * 4;
-          f32x4 part[DPT / 4];
+        float Mr = kNegInf;
+        for (int sp = 0; sp < nsplit; sp += MS) {
+          f32x4 pt[MS][DPT / 4];
+          float m[MS], l[MS];
 #pragma unroll
-          for (int i = 0; i < DPT / 4; ++i)
-            part[i] = load_coherent16(rr, rb + (2 * COLS + cl * D + d0 + 4 * i) * 4);
-          const float m = load_coherent4(rr, rb + cl * 4);
-          const float l = load_coherent4(rr, rb + (COLS + cl) * 4);
+          for (int k = 0; k < MS; ++k) {
+            const bool in = sp + k < nsplit;
+            const int rb = (in ? sp + k : sp) * REC * 4;
+#pragma unroll
+            for (int i = 0; i < DPT / 4; ++i)
+              pt[k][i] = load_coherent16(rr, rb + (2 * COLS + cl * D + d0 + 4 * i) * 4);
+            m[k] = in ? load_coherent4(rr, rb + cl * 4) : kNegInf;
+            l[k] = in ? load_coherent4(rr, rb + (COLS + cl) * 4) : 0.f;
+          }
           // A split that saw no key of this column has m = -inf and l = 0.
-          const float w = m == kNegInf ? 0.f : fast_exp2(m - M);
-          L += l * w;
+          float mn = Mr;
 #pragma unroll
-          for (int i = 0; i < DPT / 4; ++i) v[i] += w * part[i];
+          for (int k = 0; k < MS; ++k) mn = fmaxf(mn, m[k]);
+          if (mn == kNegInf) continue;
+          const float al = Mr == kNegInf ? 0.f : fast_exp2(Mr - mn);
+          L *= al;
+#pragma unroll
+          for (int i = 0; i < DPT / 4; ++i) v[i] *= al;
+#pragma unroll
+          for (int k = 0; k < MS; ++k) {
+            const float w = m[k] == kNegInf ? 0.f : fast_exp2(m[k] - mn);
+            L += l[k] * w;
+#pragma unroll
+            for (int i = 0; i < DPT / 4; ++i) v[i] += w * pt[k][i];
+          }
+          Mr = mn;
         }
         L = 1.f / L;
       }
