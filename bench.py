@@ -118,6 +118,7 @@ def decode_benchmark(dev, seed, batch, steps):
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
     timed = steps - warm
+    attn_ms = attention_share_ms(dev, runner, seqs)
     return {
         "tokens_per_s": round(batch * timed / dt, 1),
         "ms_per_step": round(1e3 * dt / timed, 3),
@@ -125,6 +126,8 @@ def decode_benchmark(dev, seed, batch, steps):
         "decode_steps_timed": timed,
         "warmup_steps": warm,
         "prefill_s": round(prefill_s, 3),
+        "attention_ms_per_step": round(attn_ms, 3),
+        "attention_share": round(attn_ms / (1e3 * dt / timed), 3),
         "model": "Qwen2.5-0.5B architecture, random init N(0, 0.02), fp16, untied lm_head",
         "prompt_lens": "U[64, 1024], random token ids",
     }
@@ -180,6 +183,46 @@ def prefill_benchmark(dev, seed, B=8, cached=2048, new=512, iters=30, warmup=5):
         "roofline": {"bound": "mfma", "achieved": round(tflops, 1), "peak": MFMA_F16_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(tflops / MFMA_F16_PEAK_TFLOPS, 4)},
     }
+
+
+def attention_share_ms(dev, runner, seqs, iters=20):
+    """The decode step's paged-attention work timed on its own: per layer one fused RoPE +
+    K/V write and one batched attention call at the batch's final lengths, times the layers.
+
+    Synthetic q/k/v/cos/sin of the step's shapes; layer 0's pool is written (after the
+    timed steps, so nothing measured reads it).
+    """
+    import torch
+
+    from engine.kernels.paged_attention import paged_attention_decode_batched, pad_block_tables
+    from engine.kernels.paged_attention_integration import paged_rope_kv_write
+
+    b = len(seqs)
+    hq, hkv, d = QWEN05["num_attention_heads"], QWEN05["num_key_value_heads"], runner.head_dim
+    tables = pad_block_tables([s.block_table.physical_block_ids for s in seqs], device=dev)
+    lens = torch.tensor([s.block_table.num_tokens for s in seqs], dtype=torch.int32, device=dev)
+    g = torch.Generator(device=dev).manual_seed(5)
+    q = torch.randn(b, hq, d, generator=g, device=dev).half()
+    k = torch.randn(b, hkv, d, generator=g, device=dev).half()
+    v = torch.randn(b, hkv, d, generator=g, device=dev).half()
+    cos = torch.rand(b, d, generator=g, device=dev).half()
+    sin = torch.rand(b, d, generator=g, device=dev).half()
+    kc, vc = runner.pool.k_cache[0], runner.pool.v_cache[0]
+
+    def layer():
+        qr = paged_rope_kv_write(q, k, v, cos, sin, kc, vc, tables, lens)
+        return paged_attention_decode_batched(qr, kc, vc, tables, lens, d ** -0.5)
+
+    for _ in range(3):
+        layer()
+    torch.cuda.synchronize()
+    a, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(iters):
+        layer()
+    e.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(e) / iters * QWEN05["num_hidden_layers"]
 
 
 def make_workload(name, device, seed):
