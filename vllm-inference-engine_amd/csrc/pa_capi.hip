@@ -695,6 +695,14 @@ int pa_prefill_attention_f16(const void* q, const int64_t q_strides[3], const vo
     set_error("scale must be positive and finite");
     return PA_ERR_ARG;
   }
+  // The kernel's per-piece address arithmetic is 32-bit inside a block.
+  const int64_t lim = 0x7fffffff;
+  if (k_strides[0] > 0xffffffffll || v_strides[0] > 0xffffffffll ||
+      k_strides[1] * block_size + head_dim > lim || v_strides[1] * block_size + head_dim > lim ||
+      bt_strides[1] < 0 || bt_strides[1] * (int64_t)max_blocks_per_seq > lim) {
+    set_error("cache block stride must fit 32 bits and row / table offsets 31 bits");
+    return PA_ERR_UNSUPPORTED;
+  }
   const int g = num_q_heads / num_kv_heads;
   const PrefillPlan plan = prefill_plan(num_seqs, num_q_heads, num_kv_heads, head_dim, block_size,
                                         max_blocks_per_seq, max_query_len);

@@ -131,24 +131,31 @@ __global__ __launch_bounds__(256) void prefill_attn_kernel(PrefillAttnArgs a) {
   // Piece f = 256 i + tid of a tile is key row f / CPR, halves (f % CPR) * 8.
   // The block ids of a tile are loaded one tile before its K/V, so a K/V load
   // never waits on the table read it depends on.
+  // Element strides fit 32 bits (the host checks it): a block's offset is one
+  // 32 x 32 -> 64-bit multiply-add, the row offset inside it 32-bit. This
+  // address arithmetic runs for every 16-byte piece of every tile, so it is
+  // kept to a few instructions.
+  const uint32_t k_sb = (uint32_t)a.k_sb, v_sb = (uint32_t)a.v_sb;
+  const uint32_t k_st = (uint32_t)a.k_st, v_st = (uint32_t)a.v_st;
+  const uint32_t bt_sk = (uint32_t)a.bt_sk;
   auto fetch_ids = [&](int kt) {
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
       const int key = kt * KT + (i * 64 * NW + tid) / CPR;
-      ids[i] = key < kmax ? btrow[(int64_t)(key / bs) * a.bt_sk] : 0;
+      ids[i] = key < kmax ? btrow[(uint32_t)(key / bs) * bt_sk] : 0;
     }
   };
   auto fetch_kv = [&](int kt) {
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
       const int f = i * 64 * NW + tid;
-      const int c8 = (f % CPR) * 8;
+      const uint32_t c8 = (f % CPR) * 8;
       const int key = kt * KT + f / CPR;
       if (key < kmax) {
-        const int64_t id = min(max(ids[i], 0), a.num_blocks - 1);
-        const int64_t off = key % bs;
-        kr[i] = *reinterpret_cast<const u32x4*>(kbase + id * a.k_sb + off * a.k_st + c8);
-        vr[i] = *reinterpret_cast<const u32x4*>(vbase + id * a.v_sb + off * a.v_st + c8);
+        const uint32_t id = (uint32_t)min(max(ids[i], 0), a.num_blocks - 1);
+        const uint32_t off = (uint32_t)(key % bs);
+        kr[i] = *reinterpret_cast<const u32x4*>(kbase + (uint64_t)id * k_sb + (off * k_st + c8));
+        vr[i] = *reinterpret_cast<const u32x4*>(vbase + (uint64_t)id * v_sb + (off * v_st + c8));
       } else {
         // Rows past the last key are zeros: masked scores give p = 0, and
         // 0 * (zero row) never makes a NaN.
@@ -231,8 +238,10 @@ __global__ __launch_bounds__(256) void prefill_attn_kernel(PrefillAttnArgs a) {
     for (int cg = 0; cg < CG; ++cg) {
       float m = kNegInf;
 #pragma unroll
-      for (int s = 0; s < NS; ++s)
-        m = fmaxf(fmaxf(m, fmaxf(sc[cg][s][0], sc[cg][s][1])), fmaxf(sc[cg][s][2], sc[cg][s][3]));
+      for (int s = 0; s < NS; ++s) {
+        m = fmaxf(fmaxf(m, sc[cg][s][0]), sc[cg][s][1]);  // one v_max3_f32 each
+        m = fmaxf(fmaxf(m, sc[cg][s][2]), sc[cg][s][3]);
+      }
       m = fmaxf(m, __shfl_xor(m, 16));
       m = fmaxf(m, __shfl_xor(m, 32));
       mloc[cg] = m * a.scale_log2;
