@@ -138,11 +138,15 @@ __global__ __launch_bounds__(256) void prefill_attn_kernel(PrefillAttnArgs a) {
   const uint32_t k_sb = (uint32_t)a.k_sb, v_sb = (uint32_t)a.v_sb;
   const uint32_t k_st = (uint32_t)a.k_st, v_st = (uint32_t)a.v_st;
   const uint32_t bt_sk = (uint32_t)a.bt_sk;
+  // Rows past the last key are loaded from the last key's row instead
+  // (clamped, so every load is a valid pool row and no branch splits the
+  // loads): their scores fall past every column's position and are masked,
+  // and p = 0 times a finite row adds nothing.
   auto fetch_ids = [&](int kt) {
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
-      const int key = kt * KT + (i * 64 * NW + tid) / CPR;
-      ids[i] = key < kmax ? btrow[(uint32_t)(key / bs) * bt_sk] : 0;
+      const int key = min(kt * KT + (i * 64 * NW + tid) / CPR, kmax - 1);
+      ids[i] = btrow[(uint32_t)(key / bs) * bt_sk];
     }
   };
   auto fetch_kv = [&](int kt) {
@@ -150,18 +154,11 @@ __global__ __launch_bounds__(256) void prefill_attn_kernel(PrefillAttnArgs a) {
     for (int i = 0; i < PER; ++i) {
       const int f = i * 64 * NW + tid;
       const uint32_t c8 = (f % CPR) * 8;
-      const int key = kt * KT + f / CPR;
-      if (key < kmax) {
-        const uint32_t id = (uint32_t)min(max(ids[i], 0), a.num_blocks - 1);
-        const uint32_t off = (uint32_t)(key % bs);
-        kr[i] = *reinterpret_cast<const u32x4*>(kbase + (uint64_t)id * k_sb + (off * k_st + c8));
-        vr[i] = *reinterpret_cast<const u32x4*>(vbase + (uint64_t)id * v_sb + (off * v_st + c8));
-      } else {
-        // Rows past the last key are zeros: masked scores give p = 0, and
-        // 0 * (zero row) never makes a NaN.
-        kr[i] = u32x4{0u, 0u, 0u, 0u};
-        vr[i] = u32x4{0u, 0u, 0u, 0u};
-      }
+      const int key = min(kt * KT + f / CPR, kmax - 1);
+      const uint32_t id = (uint32_t)min(max(ids[i], 0), a.num_blocks - 1);
+      const uint32_t off = (uint32_t)(key % bs);
+      kr[i] = *reinterpret_cast<const u32x4*>(kbase + (uint64_t)id * k_sb + (off * k_st + c8));
+      vr[i] = *reinterpret_cast<const u32x4*>(vbase + (uint64_t)id * v_sb + (off * v_st + c8));
     }
   };
   auto stash = [&](int buf) {
@@ -203,7 +200,8 @@ __global__ __launch_bounds__(256) void prefill_attn_kernel(PrefillAttnArgs a) {
 
     // Raw scores of the whole tile, without branches: lane (row, grp) holds
     // keys 16 s + 4 grp + r of its column in each group. Rows past the last
-    // key are zeros in LDS; the mask below removes them with the causal cut.
+    // key hold copies of the last key's row; the mask below removes them
+    // with the causal cut.
     f32x4 sc[CG][NS];
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
