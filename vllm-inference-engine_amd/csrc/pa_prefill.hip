@@ -42,10 +42,6 @@ __global__ __launch_bounds__(256) void prefill_attn_kernel(PrefillAttnArgs a) {
   constexpr int CPR = D / 8;          // 16-byte pieces per key row of one head
   constexpr int PER = KT * CPR / (64 * NW);
   constexpr int BUF = KT * LS;        // halves of one staged K (or V) tile
-  // Lazy rescaling: the running maximum is raised only when a tile's maximum
-  // exceeds it by more than this (exp2 units), so probabilities stay <= 2^8
-  // and most tiles skip the rescale of the accumulators.
-  constexpr float kLazy = 8.f;
   static_assert(PER * 64 * NW == KT * CPR, "a tile must split evenly over the workgroup");
   static_assert(NS % 2 == 0, "sub-tiles are paired for the P V products");
 
@@ -226,29 +222,56 @@ __global__ __launch_bounds__(256) void prefill_attn_kernel(PrefillAttnArgs a) {
           for (int r = 0; r < 4; ++r)
             if (kt * KT + s * 16 + grp * 4 + r > pos_c[cg]) sc[cg][s][r] = kNegInf;
     }
-    // Maxima in the exp2 domain (the scale is positive, so it commutes with
-    // the maximum). A column whose keys in this split are all masked so far
-    // keeps -inf (only possible in a split after the first, since key 0 is
-    // visible to every column).
-    float mloc[CG];
-    bool raise = false;
-#pragma unroll
-    for (int cg = 0; cg < CG; ++cg) {
-      float m = kNegInf;
-#pragma unroll
-      for (int s = 0; s < NS; ++s) {
-        m = fmaxf(fmaxf(m, sc[cg][s][0]), sc[cg][s][1]);  // one v_max3_f32 each
-        m = fmaxf(fmaxf(m, sc[cg][s][2]), sc[cg][s][3]);
-      }
-      m = fmaxf(m, __shfl_xor(m, 16));
-      m = fmaxf(m, __shfl_xor(m, 32));
-      mloc[cg] = m * a.scale_log2;
-      raise |= mloc[cg] > m_run[cg] + kLazy;
-    }
-    if (__builtin_amdgcn_ballot_w64(raise) != 0) {  // wavefront-uniform
+    // Probabilities with the running maximum as it stands. The maxima are
+    // taken only when that fails: for a column's first tile (its maximum is
+    // still -inf) or when a score exceeds it by 16 or more, so that a
+    // probability overflows fp16 -- which makes the fp16 denominator sum
+    // infinite (or NaN). Probabilities thus stay below 2^16, and most tiles
+    // skip the maxima and the accumulator rescale.
+    f16x8 pb[NS / 2][CG];
+    float lt[CG];
+    auto probs = [&]() {
 #pragma unroll
       for (int cg = 0; cg < CG; ++cg) {
-        const float m_new = fmaxf(m_run[cg], mloc[cg]);
+        // A column with no visible key yet keeps m = -inf; any finite offset
+        // then gives p = 0 for its -inf scores.
+        const float nm = m_run[cg] == kNegInf ? 0.f : -m_run[cg];
+        lt[cg] = 0.f;
+#pragma unroll
+        for (int sp = 0; sp < NS / 2; ++sp) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            pb[sp][cg][r] = (f16)fast_exp2(__builtin_fmaf(sc[cg][2 * sp][r], a.scale_log2, nm));
+            pb[sp][cg][4 + r] =
+                (f16)fast_exp2(__builtin_fmaf(sc[cg][2 * sp + 1][r], a.scale_log2, nm));
+          }
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            lt[cg] = __builtin_amdgcn_fdot2(f16x2{pb[sp][cg][2 * i], pb[sp][cg][2 * i + 1]},
+                                            f16x2{(f16)1.f, (f16)1.f}, lt[cg], false);
+        }
+      }
+    };
+    probs();
+    bool redo = false;
+#pragma unroll
+    for (int cg = 0; cg < CG; ++cg)
+      redo |= m_run[cg] == kNegInf ||
+              (__builtin_bit_cast(uint32_t, lt[cg]) & 0x7f800000u) == 0x7f800000u;
+    if (__builtin_amdgcn_ballot_w64(redo) != 0) {  // wavefront-uniform
+      // Maxima in the exp2 domain (the scale is positive, so it commutes
+      // with the maximum), raise, rescale, recompute.
+#pragma unroll
+      for (int cg = 0; cg < CG; ++cg) {
+        float m = kNegInf;
+#pragma unroll
+        for (int s = 0; s < NS; ++s) {
+          m = fmaxf(fmaxf(m, sc[cg][s][0]), sc[cg][s][1]);  // one v_max3_f32 each
+          m = fmaxf(fmaxf(m, sc[cg][s][2]), sc[cg][s][3]);
+        }
+        m = fmaxf(m, __shfl_xor(m, 16));
+        m = fmaxf(m, __shfl_xor(m, 32));
+        const float m_new = fmaxf(m_run[cg], m * a.scale_log2);
         // A column with no visible key yet (only in a split after the first)
         // stays at -inf, and -inf - -inf would make its alpha NaN.
         const float alpha = m_new == kNegInf ? 1.f : fast_exp2(m_run[cg] - m_new);
@@ -257,7 +280,10 @@ __global__ __launch_bounds__(256) void prefill_attn_kernel(PrefillAttnArgs a) {
         for (int nd = 0; nd < ND; ++nd) acc[cg][nd] *= alpha;
         m_run[cg] = m_new;
       }
+      probs();
     }
+#pragma unroll
+    for (int cg = 0; cg < CG; ++cg) l_run[cg] += lt[cg];
 
     // O^T += V^T P^T over pairs of sub-tiles, 32 keys per MFMA: operand index
     // k = 8 grp + i stands for key 16 s0 + 4 grp + i (i < 4) or 16 s1 + 4 grp
@@ -265,26 +291,9 @@ __global__ __launch_bounds__(256) void prefill_attn_kernel(PrefillAttnArgs a) {
     // fp16-rounded probabilities the products use.
 #pragma unroll
     for (int sp = 0; sp < NS / 2; ++sp) {
-      const int s0 = 2 * sp, s1 = 2 * sp + 1;
-      f16x8 pb[CG];
-#pragma unroll
-      for (int cg = 0; cg < CG; ++cg) {
-        // With no visible key yet every score is -inf; any finite offset then
-        // gives p = 0 (-inf - -inf would be NaN).
-        const float nm = m_run[cg] == kNegInf ? 0.f : -m_run[cg];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          pb[cg][r] = (f16)fast_exp2(__builtin_fmaf(sc[cg][s0][r], a.scale_log2, nm));
-          pb[cg][4 + r] = (f16)fast_exp2(__builtin_fmaf(sc[cg][s1][r], a.scale_log2, nm));
-        }
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          l_run[cg] = __builtin_amdgcn_fdot2(f16x2{pb[cg][2 * i], pb[cg][2 * i + 1]},
-                                             f16x2{(f16)1.f, (f16)1.f}, l_run[cg], false);
-      }
       // V^T operand: lane (row, grp) needs V[16 s + 4 grp + r][16 nd + row],
       // r = 0..3, which one transposing read of four key rows delivers.
-      const f16* v0 = vt_lds + (s0 * 16 + grp * 4 + (row >> 2)) * LS + (row & 3) * 4;
+      const f16* v0 = vt_lds + (2 * sp * 16 + grp * 4 + (row >> 2)) * LS + (row & 3) * 4;
       const f16* v1 = v0 + 16 * LS;
 #pragma unroll
       for (int nd = 0; nd < ND; ++nd) {
@@ -293,7 +302,7 @@ __global__ __launch_bounds__(256) void prefill_attn_kernel(PrefillAttnArgs a) {
         const f16x8 av = {a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
 #pragma unroll
         for (int cg = 0; cg < CG; ++cg)
-          acc[cg][nd] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, pb[cg], acc[cg][nd], 0, 0, 0);
+          acc[cg][nd] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, pb[sp][cg], acc[cg][nd], 0, 0, 0);
       }
     }
 
