@@ -69,6 +69,7 @@ class FakePrefillModel:
                  past_key_values=None, logits_to_keep=0):
         self.calls.append({"input_ids": input_ids.clone(), "position_ids": position_ids,
                            "past_key_values": past_key_values, "logits_to_keep": logits_to_keep,
+                           "attention_mask": attention_mask,
                            "inference_mode": torch.is_inference_mode_enabled()})
         n = input_ids.shape[1]
         pos = (position_ids[0] if position_ids is not None
@@ -145,3 +146,38 @@ def test_full_prefill_uses_cached_prefix_and_only_forwards_suffix(cuda_device):
     assert call["logits_to_keep"] == 1 and call["inference_mode"]
     assert runner.pool.k_cache[0][1].float().cpu()[:, 0, :2].tolist() == [[2, 3], [3, 4]]
     assert runner.pool.v_cache[0][1].float().cpu()[:, 0, :2].tolist() == [[102, 103], [103, 104]]
+
+
+def test_full_prefill_with_zero_hit_uses_normal_full_prompt_path(cuda_device):
+    """Reference fixture :129-151: no cached tokens in "full" mode forwards the whole prompt."""
+    from engine.memory.block_pool import BlockTable
+
+    model = FakePrefillModel(cuda_device)
+    runner = _runner(model, "full", cuda_device)
+    table = BlockTable(seq_id=0, block_size=2, physical_block_ids=[0, 1], num_tokens=3)
+    seq = SimpleNamespace(prompt_token_ids=[10, 11, 12], block_table=table, num_cached_tokens=0,
+                          last_logits=None, last_logit_margin=None)
+    runner.prefill(seq)
+    assert model.calls[0]["input_ids"].tolist() == [[10, 11, 12]]
+    assert model.calls[0]["past_key_values"] is None
+    assert model.calls[0]["inference_mode"]
+
+
+def test_full_prefill_handles_cached_prefix_and_single_remaining_token(cuda_device):
+    """Reference fixture :154-182: one block cached, one prompt token left to forward."""
+    from engine.memory.block_pool import BlockTable
+
+    model = FakePrefillModel(cuda_device)
+    runner = _runner(model, "full", cuda_device)
+    table = BlockTable(seq_id=0, block_size=2, physical_block_ids=[0, 1], num_tokens=3)
+    runner.pool.k_cache[0][0, :, 0, :2] = torch.tensor([[0, 1], [1, 2]], dtype=torch.float16)
+    runner.pool.v_cache[0][0, :, 0, :2] = torch.tensor([[100, 101], [101, 102]], dtype=torch.float16)
+    seq = SimpleNamespace(prompt_token_ids=[10, 11, 12], block_table=table, num_cached_tokens=2,
+                          last_logits=None, last_logit_margin=None)
+    runner.prefill(seq)
+    call = model.calls[0]
+    assert call["input_ids"].tolist() == [[12]]
+    assert call["position_ids"].tolist() == [[2]]
+    assert torch.equal(call["attention_mask"].cpu(), torch.ones((1, 3), dtype=torch.long))
+    assert call["past_key_values"].get_seq_length() == 3
+    assert call["inference_mode"]

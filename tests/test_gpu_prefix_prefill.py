@@ -80,6 +80,7 @@ def run_pair(runner, prompt_a, prompt_b, shared_blocks):
     (QWEN_HEADS, 3, 37),   # head_dim 64, g = 7 (Qwen2.5-0.5B heads)
     (QWEN_HEADS, 1, 150),
     (SMALL, 2, 16),        # head_dim 32, g = 2; the suffix fills whole blocks
+    (QWEN_HEADS, 2, 1),    # a single remaining prompt token after the cached blocks
 ])
 def test_full_mode_paged_prefill_matches_reference_path(cuda_device, cfg, cached_blocks, suffix):
     model = make_model(cfg, 7, cuda_device)
