@@ -91,11 +91,27 @@ def paged_greedy(runner, prompts, steps, forced=None):
     return [s.generated_ids for s in seqs], [torch.stack(l) for l in logits]
 
 
-def _check(model, prompts, steps, device):
+def _runner(model, device, need, bs, interleave):
     from engine.kernels.paged_attention_integration import KernelPagedManualDecode
 
-    need = sum((len(p) + steps + 15) // 16 + 1 for p in prompts)
-    runner = KernelPagedManualDecode(model, block_size=16, num_blocks=need + 8, device=str(device))
+    runner = KernelPagedManualDecode(model, block_size=bs, num_blocks=2 * need + 8, device=str(device))
+    if interleave:
+        # Every real block is followed by one taken for "another sequence", so a sequence's
+        # physical blocks are never adjacent (reference tests/test_paged_manual_decode.py:114-174).
+        take = runner.allocator.allocate
+
+        def allocate():
+            b = take()
+            take()
+            return b
+
+        runner.allocator.allocate = allocate
+    return runner
+
+
+def _check(model, prompts, steps, device, bs=16, interleave=False):
+    need = sum((len(p) + steps + bs - 1) // bs + 1 for p in prompts)
+    runner = _runner(model, device, need, bs, interleave)
     toks, _ = paged_greedy(runner, prompts, steps)
     divergences = 0
     ref_tokens = []
@@ -109,13 +125,14 @@ def _check(model, prompts, steps, device):
                                                f"{margins[i]:.4f} >= {NEAR_TIE}")
                 break
     # Teacher forcing: both paths consume the oracle's tokens; compare logits per step.
-    runner2 = KernelPagedManualDecode(model, block_size=16, num_blocks=need + 8, device=str(device))
+    runner2 = _runner(model, device, need, bs, interleave)
     _, paged_logits = paged_greedy(runner2, prompts, steps, forced=ref_tokens)
     worst = 0.0
     for p, want, got in zip(prompts, ref_tokens, paged_logits):
         _, ref_logits, _ = oracle_greedy(model, p, steps, forced=want)
         worst = max(worst, (got - ref_logits).abs().max().item())
-    print(f"[decode-step] {len(prompts)} seqs x {steps} steps: {divergences} near-tie divergences, "
+    print(f"[decode-step] {len(prompts)} seqs x {steps} steps, block {bs}"
+          f"{' interleaved' if interleave else ''}: {divergences} near-tie divergences, "
           f"teacher-forced max |logit diff| {worst:.4f}", flush=True)
     assert worst <= LOGIT_TOL
     return divergences
@@ -126,6 +143,17 @@ def test_tiny_model_greedy_and_teacher_forced(cuda_device):
     rng = np.random.default_rng(1)
     prompts = [rng.integers(0, 512, size=n).tolist() for n in (1, 5, 16, 17, 40, 100)]
     _check(model, prompts, 40, cuda_device)
+
+
+@pytest.mark.parametrize("bs,interleave", [(4, False), (4, True), (8, True)])
+def test_small_blocks_and_interleaved_allocation(cuda_device, bs, interleave):
+    """Reference tests/test_paged_manual_decode.py:78-174: with block size 4 a short prompt and its
+    generation span many blocks (every layer crosses block boundaries), and physical blocks
+    interleaved with another sequence's allocations are gathered through the table."""
+    model = make_model(TINY, 6, cuda_device)
+    rng = np.random.default_rng(6)
+    prompts = [rng.integers(0, 512, size=n).tolist() for n in (5, 9, 23)]
+    _check(model, prompts, 16, cuda_device, bs=bs, interleave=interleave)
 
 
 def test_qwen05_architecture_greedy_and_teacher_forced(cuda_device):
