@@ -221,7 +221,7 @@ using namespace pa;
 
 extern "C" {
 
-int pa_abi_version(void) { return 5; }
+int pa_abi_version(void) { return 6; }
 
 const char* pa_last_error(void) { return g_error.c_str(); }
 
@@ -749,6 +749,46 @@ int pa_prefill_attention_f16(const void* q, const int64_t q_strides[3], const vo
   a.cnt = plan.ws_bytes ? (int*)workspace : nullptr;
   a.recs = plan.ws_bytes ? (float*)((char*)workspace + plan.counter_bytes) : nullptr;
   return finish_launch(launch_prefill_attn(a, head_dim, (hipStream_t)stream));
+}
+
+int pa_rmsnorm_f16(const void* x, int64_t x_row_stride, const void* weight, void* y,
+                   int64_t y_row_stride, int rows, int hidden, float eps, void* stream) {
+  clear_error();
+  if (rows < 0 || hidden <= 0) {
+    set_error("rows must be >= 0 and hidden > 0");
+    return PA_ERR_ARG;
+  }
+  if (rows == 0) return PA_OK;
+  if (!x || !weight || !y) {
+    set_error("null pointer argument");
+    return PA_ERR_ARG;
+  }
+  if (x_row_stride < hidden || y_row_stride < hidden) {
+    set_error("row strides must be at least the hidden size");
+    return PA_ERR_ARG;
+  }
+  return finish_launch(launch_rmsnorm((const f16*)x, x_row_stride, (const f16*)weight, (f16*)y,
+                                      y_row_stride, rows, hidden, eps, (hipStream_t)stream));
+}
+
+int pa_silu_mul_f16(const void* gate_up, int64_t gate_up_row_stride, void* out,
+                    int64_t out_row_stride, int rows, int inter, void* stream) {
+  clear_error();
+  if (rows < 0 || inter <= 0) {
+    set_error("rows must be >= 0 and inter > 0");
+    return PA_ERR_ARG;
+  }
+  if (rows == 0) return PA_OK;
+  if (!gate_up || !out) {
+    set_error("null pointer argument");
+    return PA_ERR_ARG;
+  }
+  if (gate_up_row_stride < 2 * (int64_t)inter || out_row_stride < inter) {
+    set_error("gate_up rows need 2 * inter elements and out rows inter");
+    return PA_ERR_ARG;
+  }
+  return finish_launch(launch_silu_mul((const f16*)gate_up, gate_up_row_stride, (f16*)out,
+                                       out_row_stride, rows, inter, (hipStream_t)stream));
 }
 
 }  // extern "C"

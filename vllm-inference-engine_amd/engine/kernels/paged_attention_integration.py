@@ -49,6 +49,10 @@ __all__ = [
     "paged_prefill_attention_forward",
     "PagedPrefillContext",
     "patch_paged_attention",
+    "prepare_fused_layers",
+    "fused_decoder_layer_forward",
+    "rms_norm",
+    "silu_mul",
     "KernelPagedManualDecode",
 ]
 
@@ -387,26 +391,185 @@ def paged_prefill_attention_forward(
     return self.o_proj(attn_output), None
 
 
+# ---- fused layer pieces of the decode step --------------------------------------
+
+def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
+    """transformers' Qwen2RMSNorm.forward in one launch (same roundings): fp16 rows [..., H]."""
+    assert x.is_cuda and x.dtype == torch.float16 and weight.dtype == torch.float16
+    h = x.shape[-1]
+    rows = x.reshape(-1, h)
+    if rows.stride(-1) != 1:
+        rows = rows.contiguous()
+    out = torch.empty(rows.shape, dtype=torch.float16, device=x.device)
+    lib = _native.load()
+    with _on_device(x.device):
+        status = lib.pa_rmsnorm_f16(rows.data_ptr(), rows.stride(0), weight.contiguous().data_ptr(),
+                                    out.data_ptr(), out.stride(0), rows.shape[0], h, float(eps),
+                                    _native.stream_handle(x.device))
+    _native.check(status, "pa_rmsnorm_f16")
+    return out.view(x.shape)
+
+
+def silu_mul(gate_up: torch.Tensor) -> torch.Tensor:
+    """silu(gate) * up of a merged [rows, 2 * I] gate/up projection, in one launch."""
+    assert gate_up.is_cuda and gate_up.dtype == torch.float16 and gate_up.dim() == 2
+    assert gate_up.stride(-1) == 1 and gate_up.shape[1] % 2 == 0
+    inter = gate_up.shape[1] // 2
+    out = torch.empty(gate_up.shape[0], inter, dtype=torch.float16, device=gate_up.device)
+    lib = _native.load()
+    with _on_device(gate_up.device):
+        status = lib.pa_silu_mul_f16(gate_up.data_ptr(), gate_up.stride(0), out.data_ptr(),
+                                     out.stride(0), gate_up.shape[0], inter,
+                                     _native.stream_handle(gate_up.device))
+    _native.check(status, "pa_silu_mul_f16")
+    return out
+
+
+def _is_decoder_layer(m: nn.Module) -> bool:
+    attn, mlp = getattr(m, "self_attn", None), getattr(m, "mlp", None)
+    return (attn is not None and mlp is not None
+            and all(hasattr(attn, n) for n in ("q_proj", "k_proj", "v_proj", "o_proj"))
+            and all(hasattr(mlp, n) for n in ("gate_proj", "up_proj", "down_proj"))
+            and hasattr(m, "input_layernorm") and hasattr(m, "post_attention_layernorm"))
+
+
+def prepare_fused_layers(model: nn.Module) -> int:
+    """Concatenate each decoder layer's q/k/v and gate/up weights once, for the fused decode path.
+
+    The merged copies live on the layer (`_pa_fused`); the model's own modules
+    are left as they are. Returns the number of layers prepared. Inference
+    only: the copies do not follow later changes of the weights.
+    """
+    n = 0
+    if not isinstance(model, nn.Module):
+        return n
+    with torch.no_grad():
+        for m in model.modules():
+            if not _is_decoder_layer(m) or hasattr(m, "_pa_fused"):
+                continue
+            attn, mlp = m.self_attn, m.mlp
+            if getattr(mlp, "act_fn", None) is not None and \
+                    type(mlp.act_fn).__name__ not in ("SiLU", "SiLUActivation"):
+                continue
+            biases = [attn.q_proj.bias, attn.k_proj.bias, attn.v_proj.bias]
+            qkv_b = torch.cat(biases) if all(b is not None for b in biases) else None
+            if qkv_b is None and any(b is not None for b in biases):
+                continue
+            m._pa_fused = (
+                torch.cat([attn.q_proj.weight, attn.k_proj.weight, attn.v_proj.weight]).contiguous(),
+                qkv_b,
+                torch.cat([mlp.gate_proj.weight, mlp.up_proj.weight]).contiguous(),
+            )
+            n += 1
+    return n
+
+
+def fused_decoder_layer_forward(
+    self: nn.Module,
+    hidden_states: torch.Tensor,
+    attention_mask: Optional[torch.Tensor] = None,
+    position_ids: Optional[torch.Tensor] = None,
+    past_key_values: Any = None,
+    use_cache: Optional[bool] = False,
+    position_embeddings: Optional[Tuple[torch.Tensor, torch.Tensor]] = None,
+    **kwargs: Any,
+) -> torch.Tensor:
+    """One decoder layer of a decode step in nine launches instead of about thirty.
+
+    The same computation as transformers' Qwen2DecoderLayer.forward with the
+    paged attention forward patched in: RMSNorm (one kernel), the q/k/v
+    projections as one GEMM over the concatenated weights, the fused RoPE +
+    K/V write and the batched paged attention, o_proj with the residual added
+    by the GEMM (addmm), RMSNorm, gate and up as one GEMM, silu * up (one
+    kernel), down_proj with the residual added by the GEMM. Only decode steps
+    (one token per sequence, paged decode context) take this path.
+    """
+    attn = self.self_attn
+    ctx = getattr(attn, "_paged_attention_context", None)
+    if (ctx is None or not ctx.is_decode or getattr(ctx, "is_prefill", False)
+            or hidden_states.dim() != 3 or hidden_states.shape[1] != 1):
+        return self._orig_layer_forward(hidden_states, attention_mask=attention_mask,
+                                        position_ids=position_ids, past_key_values=past_key_values,
+                                        use_cache=use_cache, position_embeddings=position_embeddings,
+                                        **kwargs)
+    qkv_w, qkv_b, gu_w = self._pa_fused
+    b, _, hidden = hidden_states.shape
+    x = hidden_states.reshape(b, hidden)
+    hd = attn.head_dim
+    nq = attn.q_proj.out_features // hd
+    nkv = attn.k_proj.out_features // hd
+    xn = rms_norm(x, self.input_layernorm.weight, self.input_layernorm.variance_epsilon)
+    qkv = torch.nn.functional.linear(xn, qkv_w, qkv_b)
+    q = qkv[:, :nq * hd].view(b, nq, hd)
+    k = qkv[:, nq * hd:(nq + nkv) * hd].view(b, nkv, hd)
+    v = qkv[:, (nq + nkv) * hd:].view(b, nkv, hd)
+    cos, sin = position_embeddings
+    scale = attn.scaling if hasattr(attn, "scaling") else 1.0 / math.sqrt(hd)
+    k_cache = ctx.pool.k_cache[attn.layer_idx]
+    v_cache = ctx.pool.v_cache[attn.layer_idx]
+    if ctx.is_batched:
+        bt_2d, lens = ctx.padded_block_tables, ctx.seq_lens_tensor
+    else:
+        bt_2d = ctx.block_table_tensor.unsqueeze(0)
+        lens = torch.tensor([ctx.single_seq_len], dtype=torch.int32, device=ctx.pool.device)
+    q_rot = paged_rope_kv_write(q, k, v, cos, sin, k_cache, v_cache, bt_2d, lens)
+    o = paged_attention_decode_batched(q_rot, k_cache, v_cache, bt_2d, lens, scale)
+    h = torch.addmm(x, o.reshape(b, nq * hd), attn.o_proj.weight.t())
+    if attn.o_proj.bias is not None:
+        h = h + attn.o_proj.bias
+    hn = rms_norm(h, self.post_attention_layernorm.weight,
+                  self.post_attention_layernorm.variance_epsilon)
+    act = silu_mul(torch.nn.functional.linear(hn, gu_w))
+    out = torch.addmm(h, act, self.mlp.down_proj.weight.t())
+    return out.view(b, 1, hidden)
+
+
+def _fused_rms_norm_forward(self: nn.Module, hidden_states: torch.Tensor) -> torch.Tensor:
+    if hidden_states.dtype != torch.float16 or self.weight.dtype != torch.float16:
+        return self._orig_norm_forward(hidden_states)
+    return rms_norm(hidden_states, self.weight, self.variance_epsilon)
+
+
 @contextmanager
 def patch_paged_attention(model: nn.Module, context: PagedAttentionContext):
-    """Temporarily bind paged_decode_attention_forward on every attention module (reference :179-208)."""
-    attn_modules: List[Tuple[nn.Module, Callable]] = []
+    """Temporarily bind paged_decode_attention_forward on every attention module (reference :179-208).
+
+    For a decode context, decoder layers prepared by prepare_fused_layers()
+    also get fused_decoder_layer_forward, and RMSNorm modules (those with
+    `weight` and `variance_epsilon`) the one-launch norm, for the same
+    duration; prefill contexts keep transformers' layers and norms.
+    """
+    patched: List[Tuple[nn.Module, Callable, str]] = []
+    decode = getattr(context, "is_decode", False) and not getattr(context, "is_prefill", False)
     for module in model.modules():
         if all(hasattr(module, n) for n in ("q_proj", "k_proj", "v_proj", "o_proj")):
             orig_fwd = module.forward
             module._orig_attention_forward = orig_fwd
             module._paged_attention_context = context
             module.forward = paged_decode_attention_forward.__get__(module, module.__class__)
-            attn_modules.append((module, orig_fwd))
+            patched.append((module, orig_fwd, "attn"))
+        elif decode and hasattr(module, "_pa_fused") and _is_decoder_layer(module):
+            orig_fwd = module.forward
+            module._orig_layer_forward = orig_fwd
+            module.forward = fused_decoder_layer_forward.__get__(module, module.__class__)
+            patched.append((module, orig_fwd, "layer"))
+    if any(kind == "layer" for _, _, kind in patched):
+        for module in model.modules():
+            if hasattr(module, "variance_epsilon") and isinstance(getattr(module, "weight", None),
+                                                                  torch.Tensor):
+                orig_fwd = module.forward
+                module._orig_norm_forward = orig_fwd
+                module.forward = _fused_rms_norm_forward.__get__(module, module.__class__)
+                patched.append((module, orig_fwd, "norm"))
     try:
         yield context
     finally:
-        for module, orig_fwd in attn_modules:
+        for module, orig_fwd, kind in patched:
             module.forward = orig_fwd
-            if hasattr(module, "_orig_attention_forward"):
-                delattr(module, "_orig_attention_forward")
-            if hasattr(module, "_paged_attention_context"):
-                delattr(module, "_paged_attention_context")
+            for attr in ("_orig_attention_forward", "_paged_attention_context",
+                         "_orig_layer_forward", "_orig_norm_forward"):
+                if hasattr(module, attr):
+                    delattr(module, attr)
 
 
 def paged_prefill_copy(
@@ -566,6 +729,7 @@ class KernelPagedManualDecode:
         prefix_mode: str = "off",
         use_graphs: bool = True,
         paged_prefill: bool = True,
+        fuse_layers: bool = True,
     ):
         from ..memory.block_pool import FreeListAllocator, PhysicalBlockPool
 
@@ -602,6 +766,12 @@ class KernelPagedManualDecode:
         # kernel over the pool (True) or, as the reference does, through
         # transformers' attention over a DynamicCache copy of the prefix.
         self.paged_prefill = paged_prefill
+        # Decode steps run each decoder layer as fused_decoder_layer_forward
+        # (merged q/k/v and gate/up GEMMs, one-launch RMSNorm and SwiGLU,
+        # residual adds inside the GEMMs).
+        self.fuse_layers = fuse_layers and dtype == torch.float16
+        if self.fuse_layers:
+            prepare_fused_layers(model)
 
     # -- prefill -----------------------------------------------------------------
     def _copy_prefill_kv(self, pkv: Any, block_table: Any, prompt_len: int, skip_blocks: int = 0) -> None:
