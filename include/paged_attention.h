@@ -50,7 +50,8 @@ enum {
 
 /* ABI revision of this header; bumps whenever a signature or a workspace
  * contract changes (2: zero-initialised decode workspace; 3: pa_rope_kv_write_f16;
- * 4: pa_prefill_attention_f16; 5: its workspace; 6: pa_rmsnorm_f16, pa_silu_mul_f16). */
+ * 4: pa_prefill_attention_f16; 5: its workspace; 6: pa_rmsnorm_f16, pa_silu_mul_f16;
+ * 7: residual input of pa_rmsnorm_f16, pa_top2_f16). */
 PA_API int pa_abi_version(void);
 
 /* Message of the last failed call on this thread ("" after a success). */
@@ -234,24 +235,35 @@ PA_API int pa_prefill_attention_f16(const void* q, const int64_t q_strides[3],
                                     void* workspace, size_t workspace_bytes, void* stream);
 
 /*
- * Fused elementwise chains of the decode step's transformer layers. Neither
- * has a counterpart in the reference, whose decode step runs them as
- * transformers' separate ops (paged_attention_integration.py:620-634 calls the
- * model); each replaces one chain with one launch and the same roundings.
+ * Fused elementwise chains of the decode step. None has a counterpart in the
+ * reference, whose decode step runs them as transformers' separate ops
+ * (paged_attention_integration.py:620-634 calls the model) and its greedy
+ * selection as torch arg-max / top-k (:636-651); each replaces one chain with
+ * one launch and the same roundings.
  *
- * pa_rmsnorm_f16: y[r] = fp16(w * fp16(x[r] * rsqrt(mean(x[r]^2) + eps))),
- * mean and product in fp32 -- transformers' Qwen2RMSNorm.forward. x, w and y
- * are fp16 with unit element stride; rows are row_stride elements apart.
+ * pa_rmsnorm_f16: y[r] = fp16(w * fp16(s[r] * rsqrt(mean(s[r]^2) + eps))), mean
+ * and product in fp32 -- transformers' Qwen2RMSNorm.forward -- where s = x, or,
+ * when residual is not NULL, s = fp16(x + residual) (the decoder layer's
+ * residual add), which is also written to sum. All fp16 with unit element
+ * stride; rows are row_stride elements apart.
  *
  * pa_silu_mul_f16: out[r, i] = fp16(fp16(silu(g)) * u) with g = gate_up[r, i],
  * u = gate_up[r, inter + i], silu in fp32 -- Qwen2MLP.forward's
  * act_fn(gate_proj(x)) * up_proj(x) when gate and up come from one merged
  * projection.
+ *
+ * pa_top2_f16: per row of fp16 logits, index[r] = the first position of the
+ * maximum (torch.argmax) and top[2r], top[2r+1] = the two largest values
+ * (torch.topk(row, 2).values, a repeated maximum counted twice), as fp32.
  */
-PA_API int pa_rmsnorm_f16(const void* x, int64_t x_row_stride, const void* weight, void* y,
-                          int64_t y_row_stride, int rows, int hidden, float eps, void* stream);
+PA_API int pa_rmsnorm_f16(const void* x, int64_t x_row_stride, const void* residual,
+                          int64_t residual_row_stride, void* sum, int64_t sum_row_stride,
+                          const void* weight, void* y, int64_t y_row_stride, int rows, int hidden,
+                          float eps, void* stream);
 PA_API int pa_silu_mul_f16(const void* gate_up, int64_t gate_up_row_stride, void* out,
                            int64_t out_row_stride, int rows, int inter, void* stream);
+PA_API int pa_top2_f16(const void* logits, int64_t row_stride, int rows, int vocab,
+                       int64_t* index, float* top, void* stream);
 
 #ifdef __cplusplus
 }

@@ -14,7 +14,7 @@ from __future__ import annotations
 import pytest
 import torch
 
-from engine.kernels.paged_attention_integration import rms_norm, silu_mul
+from engine.kernels.paged_attention_integration import greedy_top2, rms_norm, silu_mul
 
 pytestmark = pytest.mark.gpu
 
@@ -61,3 +61,34 @@ def test_silu_mul_matches_transformers(cuda_device, rows, inter):
     print(f"[layer-ops] silu_mul {rows}x{inter}: max {d.max().item()} ulp, {frac:.4%} differ",
           flush=True)
     assert d.max().item() <= 1 and frac < 0.02
+
+
+@pytest.mark.parametrize("rows,hidden", [(128, 896), (2, 3000)])
+def test_residual_add_and_rms_norm(cuda_device, rows, hidden):
+    """The decoder layer's residual + x in fp16, then the norm of that sum."""
+    from transformers.models.qwen2.modeling_qwen2 import Qwen2RMSNorm
+
+    g = torch.Generator(device=cuda_device).manual_seed(hidden)
+    x = torch.randn(rows, hidden, generator=g, device=cuda_device).half()
+    res = (torch.randn(rows, hidden, generator=g, device=cuda_device) * 2).half()
+    norm = Qwen2RMSNorm(hidden, eps=1e-6).to(cuda_device).half()
+    with torch.no_grad():
+        norm.weight.copy_(torch.randn(hidden, generator=g, device=cuda_device).half())
+        want_sum = res + x
+        want = norm(want_sum)
+    got_sum, got = rms_norm(x, norm.weight, norm.variance_epsilon, residual=res)
+    assert torch.equal(got_sum, want_sum)
+    assert _ulps(got, want).max().item() <= 2
+
+
+@pytest.mark.parametrize("rows,vocab", [(128, 151936), (3, 1000), (1, 7)])
+def test_greedy_top2_matches_torch(cuda_device, rows, vocab):
+    g = torch.Generator(device=cuda_device).manual_seed(vocab)
+    logits = (torch.randn(rows, vocab, generator=g, device=cuda_device) * 3).half()
+    if vocab > 10:
+        logits[0, 5] = logits[0, 9] = 100.0  # a tied maximum: first index, margin 0
+    idx, top = greedy_top2(logits)
+    assert torch.equal(idx, torch.argmax(logits, dim=-1))
+    assert torch.equal(top, torch.topk(logits, 2, dim=-1).values.float())
+    if vocab > 10:
+        assert int(idx[0]) == 5 and float(top[0, 0] - top[0, 1]) == 0.0

@@ -221,7 +221,7 @@ using namespace pa;
 
 extern "C" {
 
-int pa_abi_version(void) { return 6; }
+int pa_abi_version(void) { return 7; }
 
 const char* pa_last_error(void) { return g_error.c_str(); }
 
@@ -751,24 +751,29 @@ int pa_prefill_attention_f16(const void* q, const int64_t q_strides[3], const vo
   return finish_launch(launch_prefill_attn(a, head_dim, (hipStream_t)stream));
 }
 
-int pa_rmsnorm_f16(const void* x, int64_t x_row_stride, const void* weight, void* y,
-                   int64_t y_row_stride, int rows, int hidden, float eps, void* stream) {
+int pa_rmsnorm_f16(const void* x, int64_t x_row_stride, const void* residual,
+                   int64_t residual_row_stride, void* sum, int64_t sum_row_stride,
+                   const void* weight, void* y, int64_t y_row_stride, int rows, int hidden,
+                   float eps, void* stream) {
   clear_error();
   if (rows < 0 || hidden <= 0) {
     set_error("rows must be >= 0 and hidden > 0");
     return PA_ERR_ARG;
   }
   if (rows == 0) return PA_OK;
-  if (!x || !weight || !y) {
+  if (!x || !weight || !y || (residual && !sum)) {
     set_error("null pointer argument");
     return PA_ERR_ARG;
   }
-  if (x_row_stride < hidden || y_row_stride < hidden) {
+  if (x_row_stride < hidden || y_row_stride < hidden ||
+      (residual && (residual_row_stride < hidden || sum_row_stride < hidden))) {
     set_error("row strides must be at least the hidden size");
     return PA_ERR_ARG;
   }
-  return finish_launch(launch_rmsnorm((const f16*)x, x_row_stride, (const f16*)weight, (f16*)y,
-                                      y_row_stride, rows, hidden, eps, (hipStream_t)stream));
+  return finish_launch(launch_rmsnorm((const f16*)x, x_row_stride, (const f16*)residual,
+                                      residual_row_stride, (f16*)sum, sum_row_stride,
+                                      (const f16*)weight, (f16*)y, y_row_stride, rows, hidden, eps,
+                                      (hipStream_t)stream));
 }
 
 int pa_silu_mul_f16(const void* gate_up, int64_t gate_up_row_stride, void* out,
@@ -787,8 +792,31 @@ int pa_silu_mul_f16(const void* gate_up, int64_t gate_up_row_stride, void* out,
     set_error("gate_up rows need 2 * inter elements and out rows inter");
     return PA_ERR_ARG;
   }
+  const bool vec = inter % 8 == 0 && gate_up_row_stride % 8 == 0 && out_row_stride % 8 == 0 &&
+                   aligned(gate_up, 16) && aligned(out, 16);
   return finish_launch(launch_silu_mul((const f16*)gate_up, gate_up_row_stride, (f16*)out,
-                                       out_row_stride, rows, inter, (hipStream_t)stream));
+                                       out_row_stride, rows, inter, vec, (hipStream_t)stream));
+}
+
+int pa_top2_f16(const void* logits, int64_t row_stride, int rows, int vocab, int64_t* index,
+                float* top, void* stream) {
+  clear_error();
+  if (rows < 0 || vocab <= 0) {
+    set_error("rows must be >= 0 and vocab > 0");
+    return PA_ERR_ARG;
+  }
+  if (rows == 0) return PA_OK;
+  if (!logits || !index || !top) {
+    set_error("null pointer argument");
+    return PA_ERR_ARG;
+  }
+  if (row_stride < vocab) {
+    set_error("row stride must be at least the vocabulary size");
+    return PA_ERR_ARG;
+  }
+  const bool vec = vocab % 8 == 0 && row_stride % 8 == 0 && aligned(logits, 16);
+  return finish_launch(launch_top2((const f16*)logits, row_stride, rows, vocab, index, top, vec,
+                                   (hipStream_t)stream));
 }
 
 }  // extern "C"

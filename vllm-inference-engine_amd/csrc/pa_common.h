@@ -175,10 +175,13 @@ hipError_t launch_prefill_copy(const PrefillCopyArgs& a, bool vec, hipStream_t s
 hipError_t launch_rope_kv_write(const RopeKVArgs& a, bool vec, hipStream_t s);
 hipError_t launch_decode_streamk(const DecodeArgs& a, int D, hipStream_t s);
 hipError_t launch_prefill_attn(const PrefillAttnArgs& a, int D, hipStream_t s);
-hipError_t launch_rmsnorm(const f16* x, int64_t xs, const f16* w, f16* y, int64_t ys, int rows,
-                          int H, float eps, hipStream_t s);
+hipError_t launch_rmsnorm(const f16* x, int64_t xs, const f16* res, int64_t rs, f16* sum,
+                          int64_t ss, const f16* w, f16* y, int64_t ys, int rows, int H,
+                          float eps, hipStream_t s);
 hipError_t launch_silu_mul(const f16* gu, int64_t gs, f16* out, int64_t os, int rows, int I,
-                           hipStream_t s);
+                           bool vec, hipStream_t s);
+hipError_t launch_top2(const f16* logits, int64_t ls, int rows, int V, int64_t* idx, float* top,
+                       bool vec, hipStream_t s);
 int streamk_head_group(int num_kv_heads, int D);
 
 // Length of sequence b clamped to [0, max_blocks * bs].

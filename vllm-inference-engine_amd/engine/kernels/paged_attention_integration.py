@@ -53,6 +53,7 @@ __all__ = [
     "fused_decoder_layer_forward",
     "rms_norm",
     "silu_mul",
+    "greedy_top2",
     "KernelPagedManualDecode",
 ]
 
@@ -393,21 +394,57 @@ def paged_prefill_attention_forward(
 
 # ---- fused layer pieces of the decode step --------------------------------------
 
-def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
-    """transformers' Qwen2RMSNorm.forward in one launch (same roundings): fp16 rows [..., H]."""
+def _rows(t: torch.Tensor) -> torch.Tensor:
+    rows = t.reshape(-1, t.shape[-1])
+    return rows if rows.stride(-1) == 1 else rows.contiguous()
+
+
+def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float,
+             residual: Optional[torch.Tensor] = None):
+    """transformers' Qwen2RMSNorm.forward in one launch (same roundings): fp16 rows [..., H].
+
+    With `residual`, the norm is taken of fp16(x + residual) -- the decoder
+    layer's residual add -- and (sum, normed) is returned.
+    """
     assert x.is_cuda and x.dtype == torch.float16 and weight.dtype == torch.float16
     h = x.shape[-1]
-    rows = x.reshape(-1, h)
-    if rows.stride(-1) != 1:
-        rows = rows.contiguous()
+    rows = _rows(x)
     out = torch.empty(rows.shape, dtype=torch.float16, device=x.device)
+    res_ptr, res_stride, sum_ptr, sum_stride, total = 0, 0, 0, 0, None
+    if residual is not None:
+        assert residual.shape == x.shape and residual.dtype == torch.float16
+        res = _rows(residual)
+        total = torch.empty(rows.shape, dtype=torch.float16, device=x.device)
+        res_ptr, res_stride = res.data_ptr(), res.stride(0)
+        sum_ptr, sum_stride = total.data_ptr(), total.stride(0)
     lib = _native.load()
     with _on_device(x.device):
-        status = lib.pa_rmsnorm_f16(rows.data_ptr(), rows.stride(0), weight.contiguous().data_ptr(),
-                                    out.data_ptr(), out.stride(0), rows.shape[0], h, float(eps),
+        status = lib.pa_rmsnorm_f16(rows.data_ptr(), rows.stride(0), res_ptr, res_stride, sum_ptr,
+                                    sum_stride, weight.contiguous().data_ptr(), out.data_ptr(),
+                                    out.stride(0), rows.shape[0], h, float(eps),
                                     _native.stream_handle(x.device))
     _native.check(status, "pa_rmsnorm_f16")
-    return out.view(x.shape)
+    if total is None:
+        return out.view(x.shape)
+    return total.view(x.shape), out.view(x.shape)
+
+
+def greedy_top2(logits: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Per row of fp16 logits [rows, vocab]: (argmax int64 [rows], top-2 values fp32 [rows, 2]).
+
+    torch.argmax (first index of the maximum) and torch.topk(row, 2).values in one launch.
+    """
+    assert logits.is_cuda and logits.dtype == torch.float16 and logits.dim() == 2
+    assert logits.stride(-1) == 1
+    rows, vocab = logits.shape
+    idx = torch.empty(rows, dtype=torch.int64, device=logits.device)
+    top = torch.empty(rows, 2, dtype=torch.float32, device=logits.device)
+    lib = _native.load()
+    with _on_device(logits.device):
+        status = lib.pa_top2_f16(logits.data_ptr(), logits.stride(0), rows, vocab, idx.data_ptr(),
+                                 top.data_ptr(), _native.stream_handle(logits.device))
+    _native.check(status, "pa_top2_f16")
+    return idx, top
 
 
 def silu_mul(gate_up: torch.Tensor) -> torch.Tensor:
@@ -479,10 +516,11 @@ def fused_decoder_layer_forward(
     The same computation as transformers' Qwen2DecoderLayer.forward with the
     paged attention forward patched in: RMSNorm (one kernel), the q/k/v
     projections as one GEMM over the concatenated weights, the fused RoPE +
-    K/V write and the batched paged attention, o_proj with the residual added
-    by the GEMM (addmm), RMSNorm, gate and up as one GEMM, silu * up (one
-    kernel), down_proj with the residual added by the GEMM. Only decode steps
-    (one token per sequence, paged decode context) take this path.
+    K/V write and the batched paged attention, o_proj, the residual add and
+    RMSNorm in one kernel, gate and up as one GEMM, silu * up (one kernel),
+    down_proj with the residual added by the GEMM into the residual sum's own
+    buffer. Only decode steps (one token per sequence, paged decode context)
+    take this path.
     """
     attn = self.self_attn
     ctx = getattr(attn, "_paged_attention_context", None)
@@ -514,14 +552,12 @@ def fused_decoder_layer_forward(
         lens = torch.tensor([ctx.single_seq_len], dtype=torch.int32, device=ctx.pool.device)
     q_rot = paged_rope_kv_write(q, k, v, cos, sin, k_cache, v_cache, bt_2d, lens)
     o = paged_attention_decode_batched(q_rot, k_cache, v_cache, bt_2d, lens, scale)
-    h = torch.addmm(x, o.reshape(b, nq * hd), attn.o_proj.weight.t())
-    if attn.o_proj.bias is not None:
-        h = h + attn.o_proj.bias
-    hn = rms_norm(h, self.post_attention_layernorm.weight,
-                  self.post_attention_layernorm.variance_epsilon)
+    proj = torch.nn.functional.linear(o.reshape(b, nq * hd), attn.o_proj.weight, attn.o_proj.bias)
+    h, hn = rms_norm(proj, self.post_attention_layernorm.weight,
+                     self.post_attention_layernorm.variance_epsilon, residual=x)
     act = silu_mul(torch.nn.functional.linear(hn, gu_w))
-    out = torch.addmm(h, act, self.mlp.down_proj.weight.t())
-    return out.view(b, 1, hidden)
+    h.addmm_(act, self.mlp.down_proj.weight.t())  # h is this layer's own buffer
+    return h.view(b, 1, hidden)
 
 
 def _fused_rms_norm_forward(self: nn.Module, hidden_states: torch.Tensor) -> torch.Tensor:
@@ -915,8 +951,15 @@ class KernelPagedManualDecode:
             with patch_paged_attention(self.model, ctx):
                 out = self.model(input_ids=input_ids, position_ids=position_ids, use_cache=False)
             logits = out.logits[:, -1, :]
-        top2 = torch.topk(logits, k=2, dim=-1).values.double()
-        both = torch.stack([torch.argmax(logits, dim=-1).double(), top2[:, 0] - top2[:, 1]])
+        if logits.dtype == torch.float16 and logits.stride(-1) == 1:
+            # torch.argmax and torch.topk(k=2) in one launch (their three
+            # multi-block reductions take about 0.17 ms at batch 128).
+            idx, top = greedy_top2(logits)
+            top2 = top.double()
+            both = torch.stack([idx.double(), top2[:, 0] - top2[:, 1]])
+        else:
+            top2 = torch.topk(logits, k=2, dim=-1).values.double()
+            both = torch.stack([torch.argmax(logits, dim=-1).double(), top2[:, 0] - top2[:, 1]])
         # float64 holds every token id exactly: tokens and margins in one transfer.
         toks, margins = both.tolist()
         for i, seq in enumerate(seqs):
