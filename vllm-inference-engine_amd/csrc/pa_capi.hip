@@ -166,6 +166,7 @@ static hipError_t launch_streamk_with(DecodeArgs& a, int num_seqs, int head_dim,
   a.seg_cost = (240 << 10) / tile_bytes;
   a.cnt = (int*)ws;
   a.recs = (float*)((char*)ws + kSkCounterBytes);
+  a.recs_bytes = (int)streamk_records_bytes(a.hkv, head_dim, bound);
   return launch_decode_streamk(a, head_dim, s);
 }
 

@@ -52,6 +52,7 @@ struct DecodeArgs {
   // Nonzero: one workgroup per (sequence, kv-head group) pair instead of
   // equal ranges of the pair list (small batches of short sequences).
   int pair_per_wg;
+  int recs_bytes;  // size of the record area at recs
 };
 
 // Stream-K limits: sequences whose tile prefix fits the LDS plan, the largest

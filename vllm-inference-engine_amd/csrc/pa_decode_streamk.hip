@@ -14,8 +14,8 @@
 // a fixed order at the end of the segment, so results are the same bits on
 // every run. A pair wholly inside the range is written as final fp16 output;
 // a pair cut by a range boundary leaves an fp32 partial record (at most two
-// per workgroup), and the last workgroup to finish such a pair combines its
-// records by log-sum-exp, in record order.
+// per workgroup), and the last workgroup to count an arrival for such a pair
+// combines its records by log-sum-exp, in record order.
 //
 // Per tile a wavefront loads the K and V rows of HG adjacent kv heads with
 // whole-cache-line, non-temporal 16-byte loads (whole contiguous token rows
@@ -39,53 +39,37 @@ __host__ __device__ inline int64_t range_start(int w, int64_t T, int G) {
   return (int64_t)w * T / G;
 }
 
-// Combines the partial records of one pair cut by workgroup range
-// boundaries: records of ranges wa..wa+nrec-1 (wa's tail slot, the others'
-// head slots), read eight at a time with every load issued before any is
-// used (device-coherent loads: the records were written on other XCDs) and
-// folded in by an online log-sum-exp. One output element per thread
-// of the calling workgroup (nthr threads).
-template <int D, int HG>
-__device__ void merge_records(const DecodeArgs& a, int b, int hgp, int wa, int nrec, int tid, int nthr) {
-  constexpr int REC = record_floats(D);
-  constexpr int BATCH = 8;
-  const int nout = HG * a.g * D;
-  for (int i = tid; i < nout; i += nthr) {
-    const int hg = i / (a.g * D);
-    const int rem = i - hg * a.g * D;
-    const int hd = rem / D;
-    const int d = rem - hd * D;
-    float M = kNegInf, num = 0.f, den = 0.f;
-    for (int k0 = 0; k0 < nrec; k0 += BATCH) {
-      float mv[BATCH], lv[BATCH], av[BATCH];
+// Exclusive prefix sums over a workgroup of NW wavefronts, PER values per
+// thread (thread t holds entries t * PER .. t * PER + PER - 1); returns the
+// total. s_tot holds NW ints; the call starts and ends with a barrier.
+template <int PER, int NW>
+__device__ inline int block_excl_sum(int (&v)[PER], int* s_tot, int lane, int wave) {
+  int local = 0;
 #pragma unroll
-      for (int j = 0; j < BATCH; ++j) {
-        const int k = k0 + j;
-        const int kk = k < nrec ? k : 0;
-        const int slot = 2 * (wa + kk) + (kk == 0 ? 1 : 0);
-        const float* r = a.recs + ((int64_t)slot * HG + hg) * REC;
-        mv[j] = load_coherent(r + hd);
-        lv[j] = load_coherent(r + 16 + hd);
-        av[j] = load_coherent(r + 32 + hd * D + d);
-        if (k >= nrec) mv[j] = kNegInf;
-      }
-      float mb = M;
+  for (int i = 0; i < PER; ++i) local += v[i];
+  int incl = local;
 #pragma unroll
-      for (int j = 0; j < BATCH; ++j) mb = fmaxf(mb, mv[j]);
-      const float sc = M == kNegInf ? 0.f : fast_exp2(M - mb);
-      num *= sc;
-      den *= sc;
-#pragma unroll
-      for (int j = 0; j < BATCH; ++j) {
-        const float w = mv[j] == kNegInf ? 0.f : fast_exp2(mv[j] - mb);
-        num += w * av[j];
-        den += w * lv[j];
-      }
-      M = mb;
-    }
-    a.out[(int64_t)b * a.o_sb + (int64_t)((hgp * HG + hg) * a.g + hd) * a.o_sh + d] =
-        (f16)(den > 0.f ? num / den : 0.f);
+  for (int off = 1; off < 64; off <<= 1) {
+    const int y = __shfl_up(incl, off);
+    if (lane >= off) incl += y;
   }
+  __syncthreads();
+  if (lane == 63) s_tot[wave] = incl;
+  __syncthreads();
+  int run = incl - local, total = 0;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) {
+    if (w < wave) run += s_tot[w];
+    total += s_tot[w];
+  }
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int t = v[i];
+    v[i] = run;
+    run += t;
+  }
+  __syncthreads();
+  return total;
 }
 
 template <int D, int NT, int BS, int HG, int NW>
@@ -112,11 +96,11 @@ void decode_streamk_kernel(DecodeArgs a) {
   constexpr int PER = kSkMaxSeqs / NTHR;  // sequences planned per thread
   constexpr int REC = record_floats(D);
   static_assert(PER * NTHR == kSkMaxSeqs, "plan layout");
-
   __shared__ __attribute__((aligned(16))) char smem[NW * WAVE_BYTES];
-  __shared__ int s_pref[kSkMaxSeqs + 1];
+  __shared__ int s_pref[kSkMaxSeqs + 1];  // sequence -> first tile position (per kv-head group)
   __shared__ int s_wtot[NW];
-  __shared__ int s_merge[2];  // pairs this workgroup completes (-1: none)
+  __shared__ int s_nmerge;                // pairs listed for merging
+  __shared__ int s_mlist[NTHR];           // pairs whose records this workgroup completed
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -139,36 +123,17 @@ void decode_streamk_kernel(DecodeArgs a) {
   // ---- plan: clamped lengths and the exclusive prefix of tiles per sequence ----
   {
     int cnt[PER];
-    int local = 0;
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
       const int b = tid * PER + i;
-      int n = 0;
-      if (b < B) n = (clamped_len(a, b) + 15) >> 4;
-      if (n > 0) n += a.seg_cost;  // pair width: its tiles plus the segment overhead
-      cnt[i] = n;
-      local += n;
+      const int n = b < B ? (clamped_len(a, b) + 15) >> 4 : 0;
+      cnt[i] = n > 0 ? n + a.seg_cost : 0;  // pair width: its tiles plus the segment overhead
     }
-    int incl = local;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-      const int y = __shfl_up(incl, off);
-      if (lane >= off) incl += y;
-    }
-    if (lane == 63) s_wtot[wave] = incl;
-    __syncthreads();
-    int run = incl - local;
-    int total = 0;
-#pragma unroll
-    for (int w = 0; w < NW; ++w) {
-      if (w < wave) run += s_wtot[w];
-      total += s_wtot[w];
-    }
+    const int total = block_excl_sum<PER, NW>(cnt, s_wtot, lane, wave);
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
       const int b = tid * PER + i;
-      if (b < B) s_pref[b] = run;
-      run += cnt[i];
+      if (b < B) s_pref[b] = cnt[i];
     }
     if (tid == 0) s_pref[B] = total;
     __syncthreads();
@@ -228,6 +193,97 @@ void decode_streamk_kernel(DecodeArgs a) {
   f16* kst = reinterpret_cast<f16*>(my_smem);  // K staging
   f16* vst = kst + VST;                          // V staging
 
+  // Partial records, two per range: slot 2 w + 1 for the pair range w cuts at
+  // its end, slot 2 w for the pair it continues from earlier ranges.
+  const auto rec_rsrc = tile_rsrc(a.recs, a.recs_bytes);
+
+  // The ranges wa .. wa + nrec - 1 a cut pair spans.
+  auto pair_span = [&](int p, int& wa, int& nrec) {
+    const int pb = p / NHG;
+    const int nt = s_pref[pb + 1] - s_pref[pb] - a.seg_cost;
+    const int64_t ps = (int64_t)NHG * s_pref[pb] + (int64_t)(p - pb * NHG) * (nt + a.seg_cost) + a.seg_cost;
+    wa = wg_of(ps, T, Ge);
+    nrec = wg_of(ps + nt - 1, T, Ge) - wa + 1;
+  };
+
+  // Arrivals this workgroup has counted and not yet resolved: thread t < npend
+  // counted one for pair s_mlist[t] and holds the value its counter increment
+  // returned.
+  int npend = 0;
+  int my_old = 0;
+
+  // Resolves the counted arrivals: a pair whose count this workgroup completed
+  // is merged here -- its records in range order, by an online log-sum-exp over
+  // 16-byte device-coherent loads (each thread four accumulators of one query
+  // head, eight records in flight), all such pairs of the workgroup at once --
+  // and its counter is reset to zero for the next launch.
+  auto resolve = [&]() {
+    const int my_pair = tid < npend ? s_mlist[tid] : 0;
+    if (tid == 0) s_nmerge = 0;
+    __syncthreads();
+    if (tid < npend) {
+      int wa, nrec;
+      pair_span(my_pair, wa, nrec);
+      if (my_old == nrec - 1) s_mlist[atomicAdd(&s_nmerge, 1)] = my_pair;
+    }
+    __syncthreads();
+    const int nmg = s_nmerge;
+    constexpr int DQ = D / 4;
+    const int per = HG * a.g * DQ;
+    for (int it = tid; it < nmg * per; it += NTHR) {
+      const int e = it / per;
+      int rem = it - e * per;
+      const int hh = rem / (a.g * DQ);
+      rem -= hh * a.g * DQ;
+      const int qr = rem / DQ;
+      const int dq = rem - qr * DQ;
+      const int p = s_mlist[e];
+      int wa, n;
+      pair_span(p, wa, n);
+      float M = kNegInf, den = 0.f;
+      f32x4 num = {0.f, 0.f, 0.f, 0.f};
+      for (int k0 = 0; k0 < n; k0 += 8) {
+        float mv[8], lv[8];
+        f32x4 av[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          const int kk = k0 + k < n ? k0 + k : 0;
+          const int slot = 2 * (wa + kk) + (kk == 0 ? 1 : 0);
+          const int base = (slot * HG + hh) * REC;
+          mv[k] = load_coherent4(rec_rsrc, 4 * (base + qr));
+          lv[k] = load_coherent4(rec_rsrc, 4 * (base + 16 + qr));
+          av[k] = load_coherent16(rec_rsrc, 4 * (base + 32 + qr * D + dq * 4));
+          if (k0 + k >= n) mv[k] = kNegInf;
+        }
+        float mb = M;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) mb = fmaxf(mb, mv[k]);
+        const float sc = M == kNegInf ? 0.f : fast_exp2(M - mb);
+        num *= sc;
+        den *= sc;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          const float wk = mv[k] == kNegInf ? 0.f : fast_exp2(mv[k] - mb);
+          num += wk * av[k];
+          den += wk * lv[k];
+        }
+        M = mb;
+      }
+      const float inv = den > 0.f ? 1.f / den : 0.f;
+      f16x4 ov;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) ov[c] = (f16)(num[c] * inv);
+      const int pb = p / NHG, hgp = p - pb * NHG;
+      *reinterpret_cast<f16x4*>(a.out + (int64_t)pb * a.o_sb +
+                                (int64_t)((hgp * HG + hh) * a.g + qr) * a.o_sh + dq * 4) = ov;
+    }
+    for (int e = tid; e < nmg; e += NTHR)
+      __hip_atomic_store(a.cnt + s_mlist[e], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    npend = 0;
+  };
+
+
   // Segment order: a range starts with at most one segment that continues a
   // pair begun in an earlier range. It is processed last, so every workgroup
   // starts on the first tiles of a pair: the leading blocks of all sequences
@@ -245,12 +301,6 @@ void decode_streamk_kernel(DecodeArgs a) {
     ++b;
     while (b < B - 1 && s_pref[b + 1] == s_pref[b]) ++b;
   }
-
-  // Pairs this workgroup left a partial record for (at most two: the pair it
-  // continues from the previous range and the pair cut at its range end), and
-  // the counter values its arrivals returned; read after the last segment.
-  int pend_pair[2] = {-1, -1};
-  int pend_old[2] = {0, 0};
 
   for (int pass = 0; pass < 2; ++pass) {
   int64_t x = pass == 0 ? cont_end : x0;
@@ -575,29 +625,28 @@ void decode_streamk_kernel(DecodeArgs a) {
             *reinterpret_cast<f16x4*>(a.out + (int64_t)b * a.o_sb +
                                       (int64_t)((h0 + hg) * a.g + row) * a.o_sh + nd * 16 + grp * 4) = o;
           } else {
-            float* rec = a.recs + ((int64_t)(wg * 2 + (first ? 1 : 0)) * HG + hg) * REC;
+            const int rb = ((wg * 2 + (first ? 1 : 0)) * HG + hg) * REC;
             if (grp == 0 && nd == 0) {
-              store_coherent(&rec[row], M);
-              store_coherent(&rec[16 + row], den);
+              store_coherent(a.recs + rb + row, M);
+              store_coherent(a.recs + rb + 16 + row, den);
             }
-#pragma unroll
-            for (int r = 0; r < 4; ++r) store_coherent(&rec[32 + row * D + nd * 16 + grp * 4 + r], num[r]);
+            store_coherent16(rec_rsrc, 4 * (rb + 32 + row * D + nd * 16 + grp * 4), num);
           }
         }
       }
       if (!(first && last)) {
         // Publish the record: every thread waits for its coherent stores to
         // complete, then one arrival is counted for the pair. The returned
-        // count is only needed after the last segment, so the atomic's latency
-        // overlaps the rest of the range.
+        // count is only needed when the workgroup resolves its arrivals, so
+        // the atomic's latency overlaps the rest of the range.
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
-        if (tid == 0) {
-          const int slot = first ? 1 : 0;
-          pend_pair[slot] = b * NHG + hg0;
-          pend_old[slot] = __hip_atomic_fetch_add(a.cnt + b * NHG + hg0, 1, __ATOMIC_RELAXED,
-                                                  __HIP_MEMORY_SCOPE_AGENT);
+        if (tid == npend) {
+          s_mlist[tid] = b * NHG + hg0;
+          my_old = __hip_atomic_fetch_add(a.cnt + b * NHG + hg0, 1, __ATOMIC_RELAXED,
+                                          __HIP_MEMORY_SCOPE_AGENT);
         }
+        ++npend;
       }
       __syncthreads();  // the merge state aliases the staging buffers of the next segment
     }
@@ -611,38 +660,10 @@ void decode_streamk_kernel(DecodeArgs a) {
 
   // ---- pairs cut by range boundaries: the last workgroup to arrive merges ----
   // A pair spanning ranges wa..wb has one record per range (wa's tail slot,
-  // the others' head slots). The workgroup whose arrival completes the count
-  // combines them by log-sum-exp and resets the counter to zero for the next
-  // launch, so the counters stay zero between launches.
-  if (tid == 0) {
-#pragma unroll
-    for (int k = 0; k < 2; ++k) {
-      int m = -1;
-      if (pend_pair[k] >= 0) {
-        const int p = pend_pair[k];
-        const int pb = p / NHG;
-        const int nt = s_pref[pb + 1] - s_pref[pb] - a.seg_cost;
-        const int64_t ps = (int64_t)NHG * s_pref[pb] + (int64_t)(p - pb * NHG) * (nt + a.seg_cost) + a.seg_cost;
-        const int need = wg_of(ps + nt - 1, T, Ge) - wg_of(ps, T, Ge) + 1;
-        if (pend_old[k] == need - 1) m = p;
-      }
-      s_merge[k] = m;
-    }
-  }
-  __syncthreads();
-#pragma unroll
-  for (int k = 0; k < 2; ++k) {
-    const int p = s_merge[k];
-    if (p < 0) continue;
-    const int pb = p / NHG;
-    const int hgp = p - pb * NHG;
-    const int nt = s_pref[pb + 1] - s_pref[pb] - a.seg_cost;
-    const int64_t ps = (int64_t)NHG * s_pref[pb] + (int64_t)hgp * (nt + a.seg_cost) + a.seg_cost;
-    const int wa = wg_of(ps, T, Ge);
-    const int nrec = wg_of(ps + nt - 1, T, Ge) - wa + 1;
-    merge_records<D, HG>(a, pb, hgp, wa, nrec, tid, NTHR);
-    if (tid == 0) __hip_atomic_store(a.cnt + p, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
+  // the others' head slots); the workgroup whose arrival completes the count
+  // combines them. A range cuts at most two pairs, so at most two arrivals
+  // are pending here.
+  resolve();
 }
 
 // ---------------------------------------------------------------------------
