@@ -255,6 +255,8 @@ PA_API int pa_prefill_attention_f16(const void* q, const int64_t q_strides[3],
  * pa_top2_f16: per row of fp16 logits, index[r] = the first position of the
  * maximum (torch.argmax) and top[2r], top[2r+1] = the two largest values
  * (torch.topk(row, 2).values, a repeated maximum counted twice), as fp32.
+ * NaN logits are skipped (torch would rank them first); a one-entry row gives
+ * top[2r+1] = -inf.
  */
 PA_API int pa_rmsnorm_f16(const void* x, int64_t x_row_stride, const void* residual,
                           int64_t residual_row_stride, void* sum, int64_t sum_row_stride,

@@ -1,6 +1,7 @@
 // C ABI of the paged-attention library: argument checks, launch geometry and
 // error reporting. Declarations: include/paged_attention.h.
 #include <stdarg.h>
+#include <atomic>
 #include <stdio.h>
 
 #include <string>
@@ -131,18 +132,19 @@ static bool streamk_ok(int num_seqs, int num_kv_heads, int head_dim) {
 // Longest pair (in 16-token tiles) that the one-workgroup-per-pair schedule takes.
 constexpr int kPairTilesMax = 128;
 
-// Compute units of the current device (cached per device).
+// Compute units of the current device (cached per device; threads that race
+// on the first query store the same value).
 static int device_cus() {
-  static int cache[64] = {0};
+  static std::atomic<int> cache[64];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cache[dev] == 0) {
-    int n = 0;
+  int n = cache[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
     if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
       n = 256;
-    cache[dev] = n;
+    cache[dev].store(n, std::memory_order_relaxed);
   }
-  return cache[dev];
+  return n;
 }
 
 // Fills the stream-K fields of `a` and launches; `ws` holds the pair counters
@@ -792,6 +794,10 @@ int pa_silu_mul_f16(const void* gate_up, int64_t gate_up_row_stride, void* out,
   if (gate_up_row_stride < 2 * (int64_t)inter || out_row_stride < inter) {
     set_error("gate_up rows need 2 * inter elements and out rows inter");
     return PA_ERR_ARG;
+  }
+  if ((int64_t)rows * inter > ((int64_t)1 << 38)) {
+    set_error("rows * inter exceeds the launch grid");
+    return PA_ERR_UNSUPPORTED;
   }
   const bool vec = inter % 8 == 0 && gate_up_row_stride % 8 == 0 && out_row_stride % 8 == 0 &&
                    aligned(gate_up, 16) && aligned(out, 16);
