@@ -46,7 +46,7 @@ def parse_args():
                         "with one pool); outside the attention events, inside ms_per_step")
     p.add_argument("--seed", type=int, default=0)
     p.add_argument("--no-cpu-baseline", action="store_true")
-    p.add_argument("--cpu-seconds", type=float, default=15.0,
+    p.add_argument("--cpu-seconds", type=float, default=10.0,
                    help="approximate CPU time budget of the oracle baseline sample")
     p.add_argument("--no-decode", action="store_true",
                    help="skip the decode-step tokens/sec measurement")
@@ -281,21 +281,32 @@ def cpu_baseline(w, budget_s):
 
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
-    order = list(range(w.num_seqs))
-    done, t_total, nbytes = [], 0.0, 0
     bs = w.k_cache.shape[1]
     hkv, d = w.k_cache.shape[2], w.k_cache.shape[3]
     hq = w.q.shape[1]
-    for i in order:
-        q, k, v, tables, lens = workloads.gather_subset(w, [i])
-        t0 = time.perf_counter()
-        naive_reference_paged_attention(q, k, v, tables, lens, w.scale)
-        t_total += time.perf_counter() - t0
-        done.append(i)
-        n = lens[0]
-        nbytes += 2 * hkv * d * 2 * n + 2 * hq * d * 2 + 4 * ((n + bs - 1) // bs) + 4
-        if t_total >= budget_s:
-            break
+    # The sequences are gathered to the host once; the timed work is the
+    # oracle over them, repeated in whole passes until about budget_s of CPU
+    # time (or until a first pass alone exceeds it, over as many sequences as
+    # fit).
+    subsets = []
+    done, t_total, nbytes, passes = [], 0.0, 0, 0
+    while t_total < budget_s and passes < 100:
+        for i in range(w.num_seqs):
+            if passes == 0:
+                subsets.append(workloads.gather_subset(w, [i]))
+            elif i >= len(subsets):
+                break
+            q, k, v, tables, lens = subsets[i]
+            t0 = time.perf_counter()
+            naive_reference_paged_attention(q, k, v, tables, lens, w.scale)
+            t_total += time.perf_counter() - t0
+            if passes == 0:
+                done.append(i)
+            n = lens[0]
+            nbytes += 2 * hkv * d * 2 * n + 2 * hq * d * 2 + 4 * ((n + bs - 1) // bs) + 4
+            if passes == 0 and t_total >= budget_s:
+                break
+        passes += 1
     return {
         "value": round(nbytes / t_total / 1e9, 4),
         "unit": "GB/s",
@@ -303,7 +314,8 @@ def cpu_baseline(w, budget_s):
         "kind": "port",
         "sample": (f"oracle literal fp16 path (per-sequence gather + einsum + softmax) over "
                    f"{len(done)} of {w.num_seqs} sequences ({sum(w.lens[i] for i in done)} tokens), "
-                   f"{t_total:.1f} s; per-sequence bytes counted without prefix sharing"),
+                   f"{passes} pass(es), {t_total:.1f} s of oracle time; per-sequence bytes counted "
+                   f"without prefix sharing"),
     }
 
 
