@@ -55,12 +55,17 @@ def test_workspace_sizes():
     assert lib.pa_decode_batched_workspace_bytes(2000, 14, 2, 64, 16, 32) == 0
     assert lib.pa_decode_v1_workspace_bytes(14, 2, 64, 16, 67) == 2 * 16 * 80 * 4
     assert lib.pa_decode_batched_workspace_bytes(8, 14, 2, 48, 16, 2048) == 0  # unsupported dim
-    # Prefill: one sequence, 512 new tokens of 2560 (7 x 512 / 128 = 28 column blocks x 2 kv
-    # heads = 56 workgroups, fewer than 3/4 of 2 x 256 slots): 20 key tiles of 128 split in 5
-    # pieces of 4; the fixed counter region (16384 ints), then 56 x 5 records of 128 columns
-    # x (64 + 2) floats.
+    # Prefill: one sequence, 512 new tokens of 2560. Two column groups per wavefront would give
+    # 7 x 512 / 128 = 28 column blocks x 2 kv heads = 56 workgroups, fewer than 64, so one group:
+    # 56 column blocks of 64 columns x 2 kv heads = 112 workgroups, fewer than 3/4 of 2 x 256
+    # slots: 20 key tiles of 128 split in 4 pieces of 5; the fixed counter region (16384 ints),
+    # then 112 x 4 records of 64 columns x (64 + 2) floats.
     assert lib.pa_prefill_attention_workspace_bytes(1, 14, 2, 64, 16, 160, 512) == \
-        16384 * 4 + 56 * 5 * 128 * 66 * 4
+        16384 * 4 + 112 * 4 * 64 * 66 * 4
+    # 1024 new tokens of 9216: 56 column blocks of 128 x 2 = 112 workgroups keep two groups;
+    # 72 key tiles in 4 pieces of 18.
+    assert lib.pa_prefill_attention_workspace_bytes(1, 14, 2, 64, 16, 576, 1024) == \
+        16384 * 4 + 112 * 4 * 128 * 66 * 4
     # 64 sequences give 3584 workgroups: no split, no workspace.
     assert lib.pa_prefill_attention_workspace_bytes(64, 14, 2, 64, 16, 160, 512) == 0
     # Short contexts (at most 4 key tiles) are never split.

@@ -144,6 +144,7 @@ struct PrefillAttnArgs {
   int64_t o_st, o_sh;
   int num_seqs, num_tokens, hkv, g, bs, num_blocks, max_blocks;
   int col_blocks;  // column blocks per (sequence, kv head): ceil(max_query_len * g / columns)
+  int col_groups;  // column groups of 16 per wavefront (columns per workgroup = 64 x this)
   float scale_log2;
   // Key-range split: a column block whose keys span more than split_tiles key
   // tiles is processed by several workgroups (up to max_splits), which leave
@@ -156,8 +157,9 @@ struct PrefillAttnArgs {
 // Column groups of 16 (token, query head) columns each prefill wavefront
 // takes (four wavefronts per workgroup): two below head_dim 256, where the
 // registers allow it, so each K and V operand read from LDS feeds two MFMAs.
+// Launches with few column blocks take one group instead (twice the
+// workgroups); see prefill_plan.
 __host__ __device__ constexpr int prefill_col_groups(int D) { return D <= 128 ? 2 : 1; }
-__host__ __device__ constexpr int prefill_cols_per_wg(int D) { return 64 * prefill_col_groups(D); }
 // The prefill workspace starts with a fixed region of arrival counters, one per
 // column block of a split launch, so that the counters of every launch sit at
 // the same place whatever its size and never overlap an earlier launch's

@@ -435,15 +435,24 @@ __global__ __launch_bounds__(256) void prefill_attn_kernel(PrefillAttnArgs a) {
   if (tid == 0) __hip_atomic_store(a.cnt + blk, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-template <int D>
-static hipError_t launch_prefill_d(const PrefillAttnArgs& a, hipStream_t s) {
+template <int D, int CG>
+static hipError_t launch_prefill_dc(const PrefillAttnArgs& a, hipStream_t s) {
   const int64_t grid = (int64_t)a.col_blocks * a.max_splits * a.num_seqs * a.hkv;
-  constexpr int CG = prefill_col_groups(D);
   if (a.bs == 16)
     hipLaunchKernelGGL((prefill_attn_kernel<D, 16, CG>), dim3((unsigned)grid), dim3(256), 0, s, a);
   else
     hipLaunchKernelGGL((prefill_attn_kernel<D, 0, CG>), dim3((unsigned)grid), dim3(256), 0, s, a);
   return hipGetLastError();
+}
+
+template <int D>
+static hipError_t launch_prefill_d(const PrefillAttnArgs& a, hipStream_t s) {
+  constexpr int CG = prefill_col_groups(D);
+  if constexpr (CG > 1) {
+    if (a.col_groups == 1) return launch_prefill_dc<D, 1>(a, s);
+  }
+  if (a.col_groups != CG) return hipErrorInvalidValue;
+  return launch_prefill_dc<D, CG>(a, s);
 }
 
 hipError_t launch_prefill_attn(const PrefillAttnArgs& a, int D, hipStream_t s) {
