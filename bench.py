@@ -48,6 +48,9 @@ def parse_args():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=10.0,
                    help="approximate CPU time budget of the oracle baseline sample")
+    p.add_argument("--decode-only", action="store_true",
+                   help="run only the decode-step tokens/sec measurement (for kernel profiles of "
+                        "the decode step) and print its result")
     p.add_argument("--no-decode", action="store_true",
                    help="skip the decode-step tokens/sec measurement")
     p.add_argument("--no-prefill", action="store_true",
@@ -113,9 +116,11 @@ def decode_benchmark(dev, seed, batch, steps):
         one_step()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
+    torch.cuda.nvtx.range_push("decode_steps")  # marks the timed steps in profiler traces
     for _ in range(steps - warm):
         one_step()
     torch.cuda.synchronize()
+    torch.cuda.nvtx.range_pop()
     dt = time.perf_counter() - t0
     timed = steps - warm
     attn_ms = attention_share_ms(dev, runner, seqs)
@@ -331,6 +336,10 @@ def main():
     from engine.kernels.paged_attention_integration import paged_kv_write
 
     dev = torch.device("cuda", 0)
+    if args.decode_only:
+        dec = decode_benchmark(dev, args.seed, args.decode_batch, args.decode_steps)
+        print(json.dumps({"decode_tokens_per_s": dec["tokens_per_s"], "decode": dec}), flush=True)
+        return
     copies = [make_workload(args.workload, dev, args.seed)]
     base = copies[0]
     for _ in range(1, max(1, args.copies)):
