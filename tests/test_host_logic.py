@@ -111,3 +111,13 @@ def test_free_list_allocator_counts_references():
     assert a.num_free == 2 and a.ref_counts == {ids[0]: 1}
     with pytest.raises(ValueError):
         a.free(ids[1])
+
+
+def test_launch_tensors_must_share_one_device():
+    """The kernels take raw device pointers: mixing devices is refused before any launch."""
+    from engine.kernels import _native
+
+    a, b = torch.zeros(2), torch.zeros(2, device="meta")
+    _native.same_device(a, torch.ones(3))
+    with pytest.raises(AssertionError, match="same device"):
+        _native.same_device(a, b)

@@ -160,6 +160,13 @@ def workspace(nbytes: int, device: torch.device, stream: int, kind: str = WS_DEC
     return buf.data_ptr()
 
 
+def same_device(*tensors: torch.Tensor) -> None:
+    """Every tensor of a launch lives on one GPU (the kernels take raw device pointers)."""
+    dev = tensors[0].device
+    assert all(t.device == dev for t in tensors), (
+        "all tensors must be on the same device: " + ", ".join(str(t.device) for t in tensors))
+
+
 def check(status: int, what: str) -> None:
     if status != PA_OK:
         msg = load().pa_last_error().decode(errors="replace")

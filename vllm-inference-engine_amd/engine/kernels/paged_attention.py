@@ -84,6 +84,7 @@ def paged_attention_decode_batched(
     """
     assert q.is_cuda and k_cache.is_cuda and v_cache.is_cuda
     assert block_tables.is_cuda and seq_lens.is_cuda
+    _native.same_device(q, k_cache, v_cache, block_tables, seq_lens)
     assert q.dtype == torch.float16 and k_cache.dtype == torch.float16 and v_cache.dtype == torch.float16
     assert block_tables.dtype == torch.int32 and seq_lens.dtype == torch.int32
 
@@ -151,6 +152,7 @@ def paged_attention_prefill(
     """
     assert q.is_cuda and k_cache.is_cuda and v_cache.is_cuda
     assert block_tables.is_cuda and seq_lens.is_cuda and query_start_loc.is_cuda
+    _native.same_device(q, k_cache, v_cache, block_tables, seq_lens, query_start_loc)
     assert q.dtype == torch.float16 and k_cache.dtype == torch.float16 and v_cache.dtype == torch.float16
     assert block_tables.dtype == torch.int32 and seq_lens.dtype == torch.int32
     assert query_start_loc.dtype == torch.int32
@@ -196,6 +198,7 @@ def paged_attention_prefill(
 
 def _single_seq_args(q, k_cache, v_cache, block_table, seq_len):
     assert q.is_cuda and k_cache.is_cuda and v_cache.is_cuda and block_table.is_cuda
+    _native.same_device(q, k_cache, v_cache, block_table)
     assert q.dtype == torch.float16 and k_cache.dtype == torch.float16 and v_cache.dtype == torch.float16
     assert block_table.dtype == torch.int32
 

@@ -87,6 +87,8 @@ def paged_kv_write(
     key = _as_rows(key)
     value = _as_rows(value)
     assert key.is_cuda and value.is_cuda and k_cache.is_cuda and v_cache.is_cuda
+    _native.same_device(key, value, k_cache, v_cache, block_tables,
+                        *([seq_lens] if isinstance(seq_lens, torch.Tensor) else []))
     assert key.dtype == torch.float16 and value.dtype == torch.float16
     assert k_cache.dtype == torch.float16 and v_cache.dtype == torch.float16
     assert block_tables.dtype == torch.int32 and block_tables.is_cuda
@@ -159,6 +161,8 @@ def paged_rope_kv_write(
     for t in (query, key, value, cos, sin, k_cache, v_cache):
         assert t.is_cuda and t.dtype == torch.float16
     assert block_tables.dtype == torch.int32 and block_tables.is_cuda
+    _native.same_device(query, key, value, cos, sin, k_cache, v_cache, block_tables,
+                        *([seq_lens] if isinstance(seq_lens, torch.Tensor) else []))
     assert k_cache.shape == v_cache.shape, "k_cache and v_cache must have the same shape"
     num_blocks, block_size, num_kv_heads, head_dim = k_cache.shape
     num_seqs, num_q_heads = query.shape[0], query.shape[1]
@@ -408,6 +412,7 @@ def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float,
     layer's residual add -- and (sum, normed) is returned.
     """
     assert x.is_cuda and x.dtype == torch.float16 and weight.dtype == torch.float16
+    _native.same_device(x, weight, *([residual] if residual is not None else []))
     h = x.shape[-1]
     rows = _rows(x)
     out = torch.empty(rows.shape, dtype=torch.float16, device=x.device)
@@ -625,6 +630,7 @@ def paged_prefill_copy(
     first, as the reference's `.to(self.dtype)` does.
     """
     assert k_cache.is_cuda and v_cache.is_cuda and block_ids.is_cuda
+    _native.same_device(k_cache, v_cache, block_ids, key, value)
     assert k_cache.dtype == torch.float16 and v_cache.dtype == torch.float16
     assert block_ids.dtype == torch.int32 and block_ids.dim() == 1
     assert k_cache.shape == v_cache.shape
