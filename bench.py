@@ -48,6 +48,10 @@ def parse_args():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=10.0,
                    help="approximate CPU time budget of the oracle baseline sample")
+    p.add_argument("--reference-grid", action="store_true",
+                   help="latency of the batched kernel over the reference's published grid "
+                        "(batch 1/4/16/32 x length 128/512/2048, cache flushed before each call) "
+                        "and print it")
     p.add_argument("--decode-only", action="store_true",
                    help="run only the decode-step tokens/sec measurement (for kernel profiles of "
                         "the decode step) and print its result")
@@ -324,6 +328,57 @@ def cpu_baseline(w, budget_s):
     }
 
 
+def reference_grid(dev, flush_mb=512):
+    """The reference's batched-kernel benchmark grid, measured the same way.
+
+    scripts/benchmark_l2_flushed_sdpa_fair.py:56-128 of the reference: 14 q / 2
+    kv heads, head_dim 64, block 16, equal lengths S, block ids shuffled over a
+    pool of B * ceil(S / 16) + 128 blocks (seed 42 + 100 B + S), 15 untimed
+    calls, then 35 calls each preceded by a buffer write that evicts the caches
+    (512 MB here, above the MI355X's 256 MB MALL), median of the events around
+    each call; bytes B*S*Hkv*D*2*2 + B*Hq*D*2*2.
+    """
+    import random
+
+    import torch
+
+    from engine.kernels.paged_attention import paged_attention_decode_batched, pad_block_tables
+
+    hq, hkv, d, bs = 14, 2, 64, 16
+    flush = torch.empty(flush_mb << 20, dtype=torch.uint8, device=dev)
+    out = []
+    for b in (1, 4, 16, 32):
+        for s_len in (128, 512, 2048):
+            q = torch.randn(b, hq, d, dtype=torch.float16, device=dev)
+            mb = (s_len + bs - 1) // bs
+            total = b * mb + 128
+            ids = list(range(total))
+            random.seed(42 + b * 100 + s_len)
+            random.shuffle(ids)
+            tables = [ids[i * mb:(i + 1) * mb] for i in range(b)]
+            kc = torch.randn(total, bs, hkv, d, dtype=torch.float16, device=dev)
+            vc = torch.randn(total, bs, hkv, d, dtype=torch.float16, device=dev)
+            bt = pad_block_tables(tables, device=dev)
+            sl = torch.full((b,), s_len, dtype=torch.int32, device=dev)
+            call = lambda: paged_attention_decode_batched(q, kc, vc, bt, sl, d ** -0.5)
+            for _ in range(15):
+                call()
+            torch.cuda.synchronize()
+            ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                  for _ in range(35)]
+            for e0, e1 in ev:
+                flush.zero_()
+                e0.record()
+                call()
+                e1.record()
+            torch.cuda.synchronize()
+            ms = statistics.median(e0.elapsed_time(e1) for e0, e1 in ev)
+            nbytes = b * s_len * hkv * d * 2 * 2 + b * hq * d * 2 * 2
+            out.append({"batch": b, "seq_len": s_len, "us": round(ms * 1e3, 2),
+                        "gbps": round(nbytes / (ms * 1e-3) / 1e9, 1)})
+    return out
+
+
 def main():
     args = parse_args()
     if args.gpus != 1:
@@ -336,6 +391,9 @@ def main():
     from engine.kernels.paged_attention_integration import paged_kv_write
 
     dev = torch.device("cuda", 0)
+    if args.reference_grid:
+        print(json.dumps({"reference_grid": reference_grid(dev)}), flush=True)
+        return
     if args.decode_only:
         dec = decode_benchmark(dev, args.seed, args.decode_batch, args.decode_steps)
         print(json.dumps({"decode_tokens_per_s": dec["tokens_per_s"], "decode": dec}), flush=True)

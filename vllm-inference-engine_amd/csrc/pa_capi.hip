@@ -131,6 +131,15 @@ static bool streamk_ok(int num_seqs, int num_kv_heads, int head_dim) {
 
 // Longest pair (in 16-token tiles) that the one-workgroup-per-pair schedule takes.
 constexpr int kPairTilesMax = 128;
+// Tables of at most this many tiles keep one workgroup per pair, and a
+// stream-K range takes at least kSkMinRange tile positions (tiles plus segment
+// overhead). Measured on MI355X (14 q / 2 kv heads, head_dim 64, block 16,
+// equal lengths, caches evicted before each call): batch 1-32 x 2048 tokens
+// 33-35 us with one workgroup per pair, 18-21 us split with ranges of at least
+// 8 positions (16: 19-21 us, 64: 25-30 us); batch 4-32 x 128 tokens 13.7-14.2
+// us one per pair, 15.8-17 us split.
+constexpr int kPairShortTiles = 16;
+constexpr int kSkMinRange = 8;
 
 // Compute units of the current device (cached per device; threads that race
 // on the first query store the same value).
@@ -155,17 +164,22 @@ static hipError_t launch_streamk_with(DecodeArgs& a, int num_seqs, int head_dim,
   const int want = kSkWgPerCu * device_cus();
   a.num_seqs = num_seqs;
   a.num_wg = want < bound ? want : bound;
-  // Pairs no longer than kPairTilesMax tiles (bounded by the table width) that
-  // all fit the GPU at once run one per workgroup: splitting them would cost
-  // more in segment starts and merges than it balances.
+  // Pairs no longer than kPairTilesMax tiles (bounded by the table width) run
+  // one per workgroup when they fill at least half the GPU, or when the table
+  // holds at most kPairShortTiles tiles: splitting them would cost more in
+  // segment starts and merges than it balances. Fewer, longer pairs are split
+  // into ranges of at least kSkMinRange tile positions.
   const int pairs = num_seqs * (a.hkv / streamk_head_group(a.hkv, head_dim));
-  a.pair_per_wg = pairs <= want && max_tiles_for(a.max_blocks, a.bs) <= kPairTilesMax;
+  const int64_t tmax = max_tiles_for(a.max_blocks, a.bs);
+  a.pair_per_wg = pairs <= want && tmax <= kPairTilesMax &&
+                  (2 * pairs >= want || tmax <= kPairShortTiles);
   if (a.pair_per_wg) a.num_wg = pairs;
   // A pair segment costs a workgroup about as long as streaming 240 KB of K/V
   // (measured on MI355X: pipeline fill plus the drain and merge across
   // wavefronts, 6-8 us per segment at the long-context shape).
   const int tile_bytes = 64 * streamk_head_group(a.hkv, head_dim) * head_dim;
   a.seg_cost = (240 << 10) / tile_bytes;
+  a.min_range = kSkMinRange;
   a.cnt = (int*)ws;
   a.recs = (float*)((char*)ws + kSkCounterBytes);
   a.recs_bytes = (int)streamk_records_bytes(a.hkv, head_dim, bound);

@@ -53,6 +53,9 @@ struct DecodeArgs {
   // equal ranges of the pair list (small batches of short sequences).
   int pair_per_wg;
   int recs_bytes;  // size of the record area at recs
+  // Stream-K ranges get at least this many tile positions each: a launch with
+  // little work uses fewer ranges than workgroups (the rest exit at once).
+  int min_range;
 };
 
 // Stream-K limits: sequences whose tile prefix fits the LDS plan, the largest

@@ -111,14 +111,6 @@ void decode_streamk_kernel(DecodeArgs a) {
   const int NHG = a.hkv / HG;
   const int bs = BS > 0 ? BS : a.bs;
   const int G = gridDim.x;
-  // Workgroup i is dispatched to XCD i % 8. Renumber so that each XCD owns a
-  // contiguous run of ranges: neighbouring sequences (which is where shared
-  // prefix blocks sit) then run on the same XCD and share its L2.
-  const int wg = [&] {
-    const int n8 = G / kXcds, rem = G % kXcds;
-    const int xcd = blockIdx.x % kXcds, k = blockIdx.x / kXcds;
-    return xcd * n8 + (xcd < rem ? xcd : rem) + k;
-  }();
 
   // ---- plan: clamped lengths and the exclusive prefix of tiles per sequence ----
   {
@@ -141,7 +133,7 @@ void decode_streamk_kernel(DecodeArgs a) {
 
   // Zero-length sequences have no tiles; their rows are written as zeros.
   const int Hq = a.hkv * a.g;
-  for (int b = wg; b < B; b += G) {
+  for (int b = blockIdx.x; b < B; b += G) {
     if (s_pref[b + 1] == s_pref[b]) {
       for (int i = tid; i < Hq * D; i += NTHR) {
         const int hq = i / D;
@@ -150,21 +142,34 @@ void decode_streamk_kernel(DecodeArgs a) {
     }
   }
 
-  // Workgroups beyond the tile count get no range, so every range is non-empty.
+  // Ranges: at least min_range tile positions each, at most one per
+  // workgroup; workgroups beyond them get no range.
   const int64_t T = (int64_t)NHG * s_pref[B];
-  const int Ge = (int)(T < G ? T : G);
+  const int64_t Gw = (T + a.min_range - 1) / a.min_range;
+  const int Ge = (int)(Gw < G ? Gw : G);  // 0 when every sequence is empty
+
+  // The first A workgroups take part. Workgroup i is dispatched to XCD i % 8;
+  // renumber the A of them so that each XCD owns a contiguous run of ranges
+  // (or pairs): neighbouring sequences, which is where shared prefix blocks
+  // sit, then run on the same XCD and share its L2, and every XCD gets work
+  // when A < G.
+  const int A = a.pair_per_wg ? (B * NHG < G ? B * NHG : G) : Ge;
+  if ((int)blockIdx.x >= A) return;
+  const int wg = [&] {
+    const int n8 = A / kXcds, rem = A % kXcds;
+    const int xcd = blockIdx.x % kXcds, k = blockIdx.x / kXcds;
+    return xcd * n8 + (xcd < rem ? xcd : rem) + k;
+  }();
   int64_t x0, x1;
   if (a.pair_per_wg) {
     // Small batches of short pairs: workgroup w takes pair w whole, so no pair
     // is cut, no partial record is written and no merge is needed.
-    if (wg >= B * NHG) return;
     const int pb = wg / NHG;
     const int width = s_pref[pb + 1] - s_pref[pb];
     if (width == 0) return;  // a zero-length sequence: its rows were written above
     x0 = (int64_t)NHG * s_pref[pb] + (int64_t)(wg - pb * NHG) * width;
     x1 = x0 + width;
   } else {
-    if (wg >= Ge) return;
     x0 = range_start(wg, T, Ge);
     x1 = range_start(wg + 1, T, Ge);
   }
