@@ -17,7 +17,7 @@ import torch  # noqa: F401  (must be loaded before the HIP library, see above)
 
 LIB_NAME = "libpa_gfx950.so"
 LIB_PATH = Path(__file__).with_name(LIB_NAME)
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 PA_OK = 0
 PA_ERR_ARG = 1
@@ -66,6 +66,9 @@ SIGNATURES: dict[str, tuple] = {
                                _vp]),
     "pa_top2_f16": (_i32, [_vp, _i64, _i32, _i32, _vp, _vp, _vp]),
     "pa_silu_mul_f16": (_i32, [_vp, _i64, _vp, _i64, _i32, _i32, _vp]),
+    "pa_linear_workspace_bytes": (_sz, [_i32, _i32, _i32, _i32, _i32]),
+    "pa_linear_f16": (_i32, [_vp, _i64, _vp, _i64, _vp, _vp, _i64, _i32, _i32, _i32, _i32, _i32,
+                              _vp, _sz, _vp]),
 }
 
 _lib = None
@@ -139,6 +142,9 @@ WS_SCORES = "scores"
 # "prefill" serves pa_prefill_attention_f16: its counters follow the same
 # zero-between-calls contract as the decode ones, with another layout.
 WS_PREFILL = "prefill"
+# "linear" serves pa_linear_f16: per-tile arrival counters (same contract),
+# then the split-K partial tiles.
+WS_LINEAR = "linear"
 
 
 def workspace(nbytes: int, device: torch.device, stream: int, kind: str = WS_DECODE) -> int | None:

@@ -468,6 +468,52 @@ def silu_mul(gate_up: torch.Tensor) -> torch.Tensor:
     return out
 
 
+LINEAR_STORE, LINEAR_ADD, LINEAR_SWIGLU = 0, 1, 2
+
+
+def linear(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor] = None, *,
+           out: Optional[torch.Tensor] = None, accumulate: bool = False, swiglu: bool = False,
+           splits: int = 0) -> torch.Tensor:
+    """A decode step's projection x W^T (pa_linear_f16), fp16 rows, fp32 accumulation.
+
+    - default: nn.functional.linear(x, weight, bias);
+    - accumulate: out.addmm_(x, weight.t()) in place (out required);
+    - swiglu: weight is a merged [gate; up] projection [2 N, K] and the result is
+      silu(x Wg^T) * (x Wu^T) [rows, N] with the MLP's fp16 roundings.
+    `splits` forces the number of workgroups sharing each output tile's K range
+    (0: chosen by the library).
+    """
+    assert x.is_cuda and x.dtype == torch.float16 and weight.dtype == torch.float16
+    assert x.dim() == 2 and weight.dim() == 2 and x.stride(1) == 1 and weight.stride(1) == 1
+    assert not (accumulate and swiglu) and (bias is None or not (accumulate or swiglu))
+    rows, k = x.shape
+    n = weight.shape[0] // 2 if swiglu else weight.shape[0]
+    assert weight.shape[1] == k and (not swiglu or weight.shape[0] % 2 == 0)
+    if accumulate:
+        assert out is not None and out.shape == (rows, n) and out.dtype == torch.float16
+        epi = LINEAR_ADD
+    else:
+        epi = LINEAR_SWIGLU if swiglu else LINEAR_STORE
+        if out is None:
+            out = torch.empty(rows, n, dtype=torch.float16, device=x.device)
+    assert out.stride(1) == 1
+    extra = [bias] if bias is not None else []
+    _native.same_device(x, weight, out, *extra)
+    if bias is not None:
+        assert bias.shape == (n,) and bias.dtype == torch.float16
+        bias = bias.contiguous()
+    lib = _native.load()
+    with _on_device(x.device):
+        stream = _native.stream_handle(x.device)
+        nbytes = lib.pa_linear_workspace_bytes(rows, n, k, epi, splits)
+        ws = _native.workspace(nbytes, x.device, stream, _native.WS_LINEAR)
+        status = lib.pa_linear_f16(x.data_ptr(), x.stride(0), weight.data_ptr(), weight.stride(0),
+                                   bias.data_ptr() if bias is not None else None, out.data_ptr(),
+                                   out.stride(0), rows, n, k, epi, splits, ws, nbytes, stream)
+    _native.check(status, "pa_linear_f16")
+    return out
+
+
 def _is_decoder_layer(m: nn.Module) -> bool:
     attn, mlp = getattr(m, "self_attn", None), getattr(m, "mlp", None)
     return (attn is not None and mlp is not None
