@@ -100,3 +100,26 @@ def test_random_shape(cuda_device, seed):
                                                compute_dtype=torch.float32)
         err = (out[pick].float().cpu() - want.float()).abs().max().item()
         assert err <= TOL, f"seed {seed}: max abs err {err:.3e}"
+
+
+@pytest.mark.parametrize("hkv,g,bs,lens", [
+    (1, 2, 4, [6, 10, 24, 300]),      # odd kv-head count: one kv head per workgroup
+    (3, 2, 8, [33, 10, 24]),
+    (1, 7, 12, [50, 1, 700]),
+    (1, 4, 1, [17, 40]),
+    (2, 2, 4, [6, 10, 24]),           # small batch: one kv head per workgroup
+    (2, 7, 8, [2000, 129, 5]),        # long pair split into stream-K ranges
+])
+def test_head_dim_32_single_head_tiles_span_blocks(cuda_device, hkv, g, bs, lens):
+    """Head_dim 32 with one kv head per workgroup: a 16-row tile is one load
+    instruction, and with blocks shorter than 16 tokens each lane's row lies in
+    its own block (every lane must look up its own row's block id)."""
+    c = dict(d=32, hkv=hkv, g=g, bs=bs, lens=lens, share=False, seed=77 + bs + hkv)
+    q, k, v, bt, sl, tables, qc, kc, vc = build(c, cuda_device)
+    print(f"[one-head tiles] hkv={hkv} g={g} bs={bs} lens={lens}", flush=True)
+    out = paged_attention_decode_batched(q, k, v, bt, sl, 32 ** -0.5)
+    torch.cuda.synchronize()
+    want = naive_reference_paged_attention(qc, kc, vc, tables, lens, 32 ** -0.5,
+                                           compute_dtype=torch.float32)
+    err = (out.float().cpu() - want.float()).abs().max().item()
+    assert err <= TOL, f"max abs err {err:.3e}"

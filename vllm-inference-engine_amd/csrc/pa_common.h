@@ -56,6 +56,7 @@ struct DecodeArgs {
   // Stream-K ranges get at least this many tile positions each: a launch with
   // little work uses fewer ranges than workgroups (the rest exit at once).
   int min_range;
+  int head_group;  // kv heads per stream-K pair (1 or 2)
 };
 
 // Stream-K limits: sequences whose tile prefix fits the LDS plan, the largest
@@ -211,7 +212,6 @@ hipError_t launch_silu_mul(const f16* gu, int64_t gs, f16* out, int64_t os, int 
 hipError_t launch_top2(const f16* logits, int64_t ls, int rows, int V, int64_t* idx, float* top,
                        bool vec, hipStream_t s);
 hipError_t launch_linear(const LinearArgs& a, int epilogue, hipStream_t s);
-int streamk_head_group(int num_kv_heads, int D);
 
 // Length of sequence b clamped to [0, max_blocks * bs].
 __device__ inline int clamped_len(const DecodeArgs& a, int b) {

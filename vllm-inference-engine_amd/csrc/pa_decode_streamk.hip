@@ -364,7 +364,9 @@ void decode_streamk_kernel(DecodeArgs a) {
         for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
           for (int j = 0; j < NID; ++j) {
-            const int t = row_token(s0 + k * NT + nt, NID == 1 ? 0 : nat_row(j));
+            // A uniform tile lies in one block; otherwise each lane looks up the
+            // block of its own row (also when one instruction covers the tile).
+            const int t = row_token(s0 + k * NT + nt, UNIFORM_TILE ? 0 : nat_row(j));
             if constexpr (UNIFORM_TILE)
               ids[nt][j] = load_uniform(btrow + (int64_t)blk_of<BS>(t, bs) * a.bt_sk);
             else
@@ -391,7 +393,7 @@ void decode_streamk_kernel(DecodeArgs a) {
 #pragma unroll
             for (int i = 0; i < NI; ++i) {
               const int t = row_token(ti, nat_row(i));
-              const int64_t id = min(max(ids[nt][NID == 1 ? 0 : i], 0), a.num_blocks - 1);
+              const int64_t id = min(max(ids[nt][i], 0), a.num_blocks - 1);
               const int64_t off = off_of<BS>(t, bs);
               const int col = nat_col(i);
               const int hg = col / D;
@@ -716,12 +718,9 @@ hipError_t launch_sk_bs(const DecodeArgs& a, hipStream_t s) {
 }  // namespace
 
 // Kv heads a wavefront handles together for this shape.
-int streamk_head_group(int num_kv_heads, int D) {
-  return (D <= 64 && num_kv_heads % 2 == 0) ? 2 : 1;
-}
-
 hipError_t launch_decode_streamk(const DecodeArgs& a, int D, hipStream_t s) {
-  const int hg = streamk_head_group(a.hkv, D);
+  const int hg = a.head_group;
+  if (hg != 1 && !(hg == 2 && D <= 64 && a.hkv % 2 == 0)) return hipErrorInvalidValue;
   switch (D) {
     case 32: return hg == 2 ? launch_sk_bs<32, 2>(a, s) : launch_sk_bs<32, 1>(a, s);
     case 64: return hg == 2 ? launch_sk_bs<64, 2>(a, s) : launch_sk_bs<64, 1>(a, s);
