@@ -43,9 +43,10 @@ def test_workspace_sizes():
     rec = (32 + 16 * 64) * 4
     counters = 65536 * 4  # per-pair arrival counters at the start of every decode workspace
     # Stream-K (<= 1024 sequences): the counters, then 2 records per workgroup of the
-    # grid bound, each covering the kv heads one wavefront handles (2 at head_dim 64).
-    # The bound is the tile count when that is smaller.
-    assert lib.pa_decode_batched_workspace_bytes(8, 14, 2, 64, 16, 32) == counters + 256 * 2 * 2 * rec
+    # grid bound, each covering the kv heads of one pair (1, or 2 at head_dim 64 when
+    # the batch's pairs outnumber the CUs). The bound is the tile count when that is
+    # smaller: 8 sequences x 2 kv heads x 32 tiles here.
+    assert lib.pa_decode_batched_workspace_bytes(8, 14, 2, 64, 16, 32) == counters + 512 * 2 * rec
     assert lib.pa_decode_batched_workspace_bytes(256, 14, 2, 64, 16, 2048) == counters + 1024 * 2 * 2 * rec
     rec128 = (32 + 16 * 128) * 4
     assert lib.pa_decode_batched_workspace_bytes(64, 28, 7, 128, 16, 128) == counters + 1024 * 2 * rec128
@@ -53,6 +54,10 @@ def test_workspace_sizes():
     # placed after the counter region so one buffer serves both paths.
     assert lib.pa_decode_batched_workspace_bytes(2000, 14, 2, 64, 16, 2048) == counters + 2000 * 2 * 64 * rec
     assert lib.pa_decode_batched_workspace_bytes(2000, 14, 2, 64, 16, 32) == 0
+    # kv heads per pair: one while sequences x kv heads stay within the CU count
+    # (256 when no GPU is visible), two above it (records hold both heads)
+    assert lib.pa_decode_batched_workspace_bytes(128, 14, 2, 64, 16, 2048) == counters + 1024 * 2 * rec
+    assert lib.pa_decode_batched_workspace_bytes(129, 14, 2, 64, 16, 2048) == counters + 1024 * 2 * 2 * rec
     assert lib.pa_decode_v1_workspace_bytes(14, 2, 64, 16, 67) == 2 * 16 * 80 * 4
     assert lib.pa_decode_batched_workspace_bytes(8, 14, 2, 48, 16, 2048) == 0  # unsupported dim
     # Prefill: one sequence, 512 new tokens of 2560. Two column groups per wavefront would give
