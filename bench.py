@@ -13,11 +13,19 @@ MALL (Infinity Cache).
 
 Output: one JSON line. value = algorithmic bytes of one attention call (K/V at
 the distinct token slots read, Q, O, table entries, lengths) / mean duration of
-the attention call measured with HIP events on the launch stream.
+the attention call measured with HIP events on the launch stream over the timed
+steps. Beside it: the median of 60 further calls, the other measured shapes
+(one Qwen2.5-0.5B layer at batch 8, the GQA sweep, the softmax stress shape,
+one layer of the batch-128 decode step), the paged prefill attention against
+the MFMA peak, decode tokens/s of the Qwen2.5-0.5B-shaped model with and
+without fused decoder layers, and the reference's CPU algorithm timed on this
+host (the oracle's fp16 and fp32 attention over the headline batch, and two
+decode steps of the whole model on the CPU).
 """
 from __future__ import annotations
 
 import argparse
+import hashlib
 import json
 import os
 import statistics
@@ -33,6 +41,11 @@ HBM_PEAK_GBS = 8000.0
 TRAFFIC_SUMMARY = REPO_ROOT / "profiles" / "long_context_traffic.md"
 
 
+def log(msg):
+    """Progress line on stderr (the JSON result is the only line on stdout)."""
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
 def parse_args():
     p = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     p.add_argument("--gpus", type=int, default=1)
@@ -46,8 +59,10 @@ def parse_args():
                         "with one pool); outside the attention events, inside ms_per_step")
     p.add_argument("--seed", type=int, default=0)
     p.add_argument("--no-cpu-baseline", action="store_true")
-    p.add_argument("--cpu-seconds", type=float, default=10.0,
-                   help="approximate CPU time budget of the oracle baseline sample")
+    p.add_argument("--cpu-seconds", type=float, default=8.0,
+                   help="approximate CPU time budget of each oracle baseline variant")
+    p.add_argument("--no-configs", action="store_true",
+                   help="skip the timings of the other measured shapes")
     p.add_argument("--reference-grid", action="store_true",
                    help="latency of the batched kernel over the reference's published grid "
                         "(batch 1/4/16/32 x length 128/512/2048, cache flushed before each call) "
@@ -64,37 +79,28 @@ def parse_args():
     return p.parse_args()
 
 
-QWEN05 = dict(vocab_size=151936, hidden_size=896, intermediate_size=4864, num_hidden_layers=24,
-              num_attention_heads=14, num_key_value_heads=2, max_position_embeddings=32768,
-              rope_theta=1e6, rms_norm_eps=1e-6, tie_word_embeddings=False)
-
-
-def decode_benchmark(dev, seed, batch, steps):
+def decode_benchmark(dev, model, prompts, steps, fuse_layers=True, attention_share=True):
     """Greedy decode of a random-init Qwen2.5-0.5B-shaped model through the paged HIP path.
 
-    batch sequences with prompt lengths U[64, 1024] of random token ids; each
-    decode step runs the model with paged_kv_write + the batched paged-attention
-    kernel in all 24 layers. Prefill (transformers forward + prefill block copy)
-    is timed separately; tokens/sec counts decode steps only.
+    len(prompts) sequences with prompt lengths U[64, 1024] of random token ids;
+    each decode step runs the model with the fused RoPE + K/V write and the
+    batched paged-attention kernel in all 24 layers, replayed as a captured
+    graph; fuse_layers also runs each decoder layer's norms, projections and
+    MLP through the fused layer forward. Prefill (transformers forward +
+    prefill block copy) is timed separately; tokens/sec counts decode steps
+    only. Returns (result, runner, seqs).
     """
-    import numpy as np
     import torch
-    from transformers import Qwen2Config, Qwen2ForCausalLM
 
     from engine.kernels.paged_attention_integration import KernelPagedManualDecode
     from engine.memory.block_pool import BlockTable
     from types import SimpleNamespace
 
-    torch.manual_seed(seed)
-    with torch.device(dev):
-        model = Qwen2ForCausalLM(Qwen2Config(**QWEN05))
-    model = model.half().eval()
-    rng = np.random.default_rng(seed)
-    lens = rng.integers(64, 1025, size=batch)
-    prompts = [rng.integers(0, QWEN05["vocab_size"], size=int(n)).tolist() for n in lens]
+    batch = len(prompts)
     bs = 16
-    need = sum((int(n) + steps + 2 * bs) // bs for n in lens)
-    runner = KernelPagedManualDecode(model, block_size=bs, num_blocks=need, device=str(dev))
+    need = sum((len(p) + steps + 2 * bs) // bs for p in prompts)
+    runner = KernelPagedManualDecode(model, block_size=bs, num_blocks=need, device=str(dev),
+                                     fuse_layers=fuse_layers)
     alloc = runner.allocator
     seqs = []
     torch.cuda.synchronize()
@@ -127,18 +133,103 @@ def decode_benchmark(dev, seed, batch, steps):
     torch.cuda.nvtx.range_pop()
     dt = time.perf_counter() - t0
     timed = steps - warm
-    attn_ms = attention_share_ms(dev, runner, seqs)
-    return {
+    res = {
         "tokens_per_s": round(batch * timed / dt, 1),
         "ms_per_step": round(1e3 * dt / timed, 3),
         "batch": batch,
         "decode_steps_timed": timed,
         "warmup_steps": warm,
         "prefill_s": round(prefill_s, 3),
-        "attention_ms_per_step": round(attn_ms, 3),
-        "attention_share": round(attn_ms / (1e3 * dt / timed), 3),
+        "fused_layers": runner.fuse_layers,
+        "graphs_captured": runner.graph_captures,
         "model": "Qwen2.5-0.5B architecture, random init N(0, 0.02), fp16, untied lm_head",
         "prompt_lens": "U[64, 1024], random token ids",
+    }
+    if attention_share:
+        attn_ms = attention_share_ms(dev, runner, seqs)
+        res["attention_ms_per_step"] = round(attn_ms, 3)
+        res["attention_share"] = round(attn_ms / (1e3 * dt / timed), 3)
+    return res, runner, seqs
+
+
+def cpu_decode_steps(model, seqs, block_size=16, steps=2):
+    """The reference's decode step on the host CPU: time `steps` steps of the whole model.
+
+    The reference runs its decode attention (integration.py:65-176) as the
+    q/k/v projections, transformers' RoPE, a per-sequence index_put K/V write
+    (:148-161) and the batched paged attention; on the CPU the attention is its
+    PyTorch algorithm (paged_attention.py:30-83). Here every attention module
+    of the same fp16 model, moved to the host, runs exactly that, with the
+    oracle's restatements of the write loop and the attention, over a pool
+    holding the decode run's block tables at its final lengths (pool values
+    synthetic: one K and one V tensor shared by the layers, the timing does
+    not depend on them). One untimed step first.
+    """
+    import torch
+    from transformers.models.qwen2.modeling_qwen2 import apply_rotary_pos_emb
+
+    from oracle.paged_attention_oracle import kv_write_reference, naive_reference_paged_attention
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    model = model.to("cpu")
+    cfg = model.config
+    bs = block_size
+    tables = [list(s.block_table.physical_block_ids) for s in seqs]
+    lens = [s.block_table.num_tokens for s in seqs]
+    nblocks = max(max(t) for t in tables) + 1
+    g = torch.Generator().manual_seed(3)
+    shape = (nblocks, bs, cfg.num_key_value_heads, cfg.hidden_size // cfg.num_attention_heads)
+    kc = torch.randn(shape, generator=g).half()
+    vc = torch.randn(shape, generator=g).half()
+
+    def attention(self, hidden_states, position_embeddings, attention_mask=None,
+                  past_key_values=None, **kwargs):
+        b = hidden_states.shape[0]
+        shp = (b, 1, -1, self.head_dim)
+        q = self.q_proj(hidden_states).view(shp).transpose(1, 2)
+        k = self.k_proj(hidden_states).view(shp).transpose(1, 2)
+        v = self.v_proj(hidden_states).view(shp).transpose(1, 2)
+        cos, sin = position_embeddings
+        q, k = apply_rotary_pos_emb(q, k, cos, sin)
+        kv_write_reference(k[:, :, 0], v[:, :, 0], kc, vc, tables, cur_lens, bs)
+        o = naive_reference_paged_attention(q[:, :, 0], kc, vc, tables, cur_lens, self.scaling)
+        return self.o_proj(o.reshape(b, 1, -1)), None
+
+    mods = [m for m in model.modules()
+            if all(hasattr(m, n) for n in ("q_proj", "k_proj", "v_proj", "o_proj"))]
+    for m in mods:
+        m.forward = attention.__get__(m, m.__class__)
+    ids = torch.randint(0, model.config.vocab_size, (len(seqs), 1), generator=g)
+    times = []
+    try:
+        with torch.inference_mode():
+            for i in range(steps + 1):
+                cur_lens = [n + 1 + i for n in lens]
+                for t, n in zip(tables, cur_lens):
+                    while len(t) * bs < n:  # a block for the new token, as the scheduler adds
+                        t.append(t[-1])
+                pos = torch.tensor([[n - 1] for n in cur_lens])
+                t0 = time.perf_counter()
+                logits = model(input_ids=ids, position_ids=pos, use_cache=False).logits
+                ids = logits[:, -1].argmax(-1, keepdim=True)
+                if i:
+                    times.append(time.perf_counter() - t0)
+    finally:
+        for m in mods:
+            del m.forward
+    t = sum(times)
+    return {
+        "tokens_per_s": round(len(seqs) * steps / t, 2),
+        "s_per_step": round(t / steps, 3),
+        "steps_timed": steps,
+        "cores": torch.get_num_threads(),
+        "batch": len(seqs),
+        "extrapolated_128_steps_s": round(128 * t / steps, 1),
+        "sample": (f"{steps} decode steps (after 1 untimed) of the same fp16 model on the host, "
+                   "each attention module running the reference's CPU algorithm (projections, "
+                   "transformers RoPE, per-sequence index_put K/V write, per-sequence gather + "
+                   "einsum + softmax); 128 steps extrapolated linearly"),
     }
 
 
@@ -205,6 +296,7 @@ def attention_share_ms(dev, runner, seqs, iters=20):
 
     from engine.kernels.paged_attention import paged_attention_decode_batched, pad_block_tables
     from engine.kernels.paged_attention_integration import paged_rope_kv_write
+    from engine.workloads import QWEN25_05B as QWEN05
 
     b = len(seqs)
     hq, hkv, d = QWEN05["num_attention_heads"], QWEN05["num_key_value_heads"], runner.head_dim
@@ -248,17 +340,32 @@ def make_workload(name, device, seed):
     raise SystemExit(f"unknown workload {name}")
 
 
+def source_digest():
+    """sha256 over the library's sources (csrc/*, include/*), names and contents, sorted."""
+    h = hashlib.sha256()
+    files = sorted((REPO_ROOT / "vllm-inference-engine_amd" / "csrc").glob("*")) + \
+        sorted((REPO_ROOT / "include").glob("*.h"))
+    for f in files:
+        h.update(f.name.encode())
+        h.update(f.read_bytes())
+    return h.hexdigest()
+
+
 def read_traffic():
-    """HBM bytes per launch from the committed rocprofv3 --pmc summary, if present."""
+    """(HBM bytes per launch, sources digest) from the committed rocprofv3 --pmc summary."""
     if not TRAFFIC_SUMMARY.exists():
-        return None
+        return None, None
+    nbytes = digest = None
     for line in TRAFFIC_SUMMARY.read_text().splitlines():
-        if line.startswith("traffic_bytes_per_launch:"):
+        key, _, val = line.partition(":")
+        if key == "traffic_bytes_per_launch":
             try:
-                return int(float(line.split(":", 1)[1].strip()))
+                nbytes = int(float(val.strip()))
             except ValueError:
-                return None
-    return None
+                nbytes = None
+        elif key == "kernel_sources_sha256":
+            digest = val.strip()
+    return nbytes, digest
 
 
 def copy_ceiling(dev, nbytes=2 << 30, iters=10):
@@ -281,50 +388,67 @@ def copy_ceiling(dev, nbytes=2 << 30, iters=10):
     return round(2 * nbytes / t / 1e9, 1)
 
 
-def cpu_baseline(w, budget_s):
-    """The oracle's literal fp16 path (the reference's CPU PyTorch algorithm) on a sample."""
-    import torch
-
+def cpu_attention_passes(w, budget_s, compute_dtype=None):
+    """The oracle's attention (the reference's CPU PyTorch algorithm) over the workload's
+    sequences, in whole passes over the batch until about budget_s of oracle time (or part of
+    one pass when a single pass exceeds it). Returns (seconds, sequences done, whole passes,
+    bytes on the per-sequence basis, unique bytes of the whole passes and their seconds)."""
     from engine import workloads
     from oracle.paged_attention_oracle import naive_reference_paged_attention
 
-    cores = len(os.sched_getaffinity(0))
-    torch.set_num_threads(cores)
     bs = w.k_cache.shape[1]
     hkv, d = w.k_cache.shape[2], w.k_cache.shape[3]
     hq = w.q.shape[1]
-    # The sequences are gathered to the host once; the timed work is the
-    # oracle over them, repeated in whole passes until about budget_s of CPU
-    # time (or until a first pass alone exceeds it, over as many sequences as
-    # fit).
-    subsets = []
-    done, t_total, nbytes, passes = [], 0.0, 0, 0
+    subsets = [workloads.gather_subset(w, [i]) for i in range(w.num_seqs)]
+    t_total, logical, passes, done, t_whole = 0.0, 0, 0, 0, 0.0
     while t_total < budget_s and passes < 100:
-        for i in range(w.num_seqs):
-            if passes == 0:
-                subsets.append(workloads.gather_subset(w, [i]))
-            elif i >= len(subsets):
-                break
-            q, k, v, tables, lens = subsets[i]
+        for q, k, v, tables, lens in subsets:
             t0 = time.perf_counter()
-            naive_reference_paged_attention(q, k, v, tables, lens, w.scale)
+            naive_reference_paged_attention(q, k, v, tables, lens, w.scale,
+                                            compute_dtype=compute_dtype)
             t_total += time.perf_counter() - t0
-            if passes == 0:
-                done.append(i)
             n = lens[0]
-            nbytes += 2 * hkv * d * 2 * n + 2 * hq * d * 2 + 4 * ((n + bs - 1) // bs) + 4
-            if passes == 0 and t_total >= budget_s:
+            logical += 2 * hkv * d * 2 * n + 2 * hq * d * 2 + 4 * ((n + bs - 1) // bs) + 4
+            if passes == 0:
+                done += 1
+            if passes == 0 and t_total >= budget_s and done < w.num_seqs:
                 break
-        passes += 1
+        else:
+            passes += 1
+            t_whole = t_total
+            continue
+        break
+    return t_total, done, passes, logical, passes * w.algorithmic_bytes(unique=True), t_whole
+
+
+def cpu_baseline(w, budget_s):
+    """The reference's CPU path on the headline batch: the oracle's literal fp16 attention
+    (value) and the same algorithm on fp32-upcast rows, each on this host's cores."""
+    import torch
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    out = {}
+    for name, dtype in (("fp16", None), ("fp32", torch.float32)):
+        t, done, passes, logical, unique, t_whole = cpu_attention_passes(w, budget_s, dtype)
+        out[name] = {
+            "gbps_unique": round(unique / t_whole / 1e9, 4) if passes else None,
+            "gbps_per_sequence": round(logical / t / 1e9, 4),
+            "seconds": round(t, 1), "passes": passes, "sequences_first_pass": done,
+        }
+    lit = out["fp16"]
+    value = lit["gbps_unique"] if lit["gbps_unique"] is not None else lit["gbps_per_sequence"]
     return {
-        "value": round(nbytes / t_total / 1e9, 4),
+        "value": value,
         "unit": "GB/s",
         "cores": torch.get_num_threads(),
         "kind": "port",
-        "sample": (f"oracle literal fp16 path (per-sequence gather + einsum + softmax) over "
-                   f"{len(done)} of {w.num_seqs} sequences ({sum(w.lens[i] for i in done)} tokens), "
-                   f"{passes} pass(es), {t_total:.1f} s of oracle time; per-sequence bytes counted "
-                   f"without prefix sharing"),
+        "sample": (f"oracle literal fp16 path (per-sequence gather + einsum + softmax) over the "
+                   f"whole headline batch ({w.num_seqs} sequences, {sum(w.lens)} tokens), "
+                   f"{lit['passes']} whole pass(es) in {lit['seconds']} s; value counts the "
+                   "GPU value's bytes (shared prefix slots once) per whole pass"),
+        "fp16": lit,
+        "fp32_upcast": out["fp32"],
     }
 
 
@@ -379,6 +503,69 @@ def reference_grid(dev, flush_mb=512):
     return out
 
 
+def clone_workload(w):
+    from engine.workloads import Workload
+
+    return Workload(name=w.name, q=w.q.clone(), k_cache=w.k_cache.clone(),
+                    v_cache=w.v_cache.clone(), block_tables=w.block_tables.clone(),
+                    seq_lens=w.seq_lens.clone(), tables=w.tables, lens=w.lens, scale=w.scale,
+                    unique_slots=w.unique_slots, meta=w.meta)
+
+
+def time_calls(copies, calls, warmup=5):
+    """HIP-event durations (ms) of `calls` attention calls rotating over the pool copies."""
+    import torch
+
+    from engine.kernels.paged_attention import paged_attention_decode_batched
+
+    def call(w):
+        return paged_attention_decode_batched(w.q, w.k_cache, w.v_cache, w.block_tables,
+                                              w.seq_lens, w.scale)
+
+    for i in range(warmup):
+        call(copies[i % len(copies)])
+    torch.cuda.synchronize()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(calls)]
+    for i, (a, b) in enumerate(ev):
+        w = copies[i % len(copies)]
+        a.record()
+        call(w)
+        b.record()
+    torch.cuda.synchronize()
+    return [a.elapsed_time(b) for a, b in ev]
+
+
+def config_timings(dev, seed, copies=4, calls=50):
+    """The other measured shapes, each over rotated pool copies: mean and median of `calls`."""
+    import torch
+
+    from engine import workloads
+
+    shapes = [("qwen_layer", lambda: workloads.qwen_layer(device=dev, seed=seed)),
+              ("softmax_stress", lambda: workloads.softmax_stress(device=dev, seed=seed)),
+              ("decode_step_layer_b128", lambda: workloads.decode_step_layer(128, dev, seed))]
+    shapes += [(f"gqa_sweep_kv{h}", lambda h=h: workloads.gqa_sweep(h, device=dev, seed=seed))
+               for h in (28, 14, 7, 4)]
+    out = {}
+    for name, make in shapes:
+        ws = [make()]
+        ws += [clone_workload(ws[0]) for _ in range(copies - 1)]
+        ms = time_calls(ws, calls)
+        nbytes = ws[0].algorithmic_bytes(unique=True)
+        mean, med = statistics.fmean(ms), statistics.median(ms)
+        out[name] = {"num_seqs": ws[0].num_seqs, "num_q_heads": ws[0].q.shape[1],
+                     "num_kv_heads": ws[0].k_cache.shape[2], "head_dim": ws[0].k_cache.shape[3],
+                     "total_tokens": sum(ws[0].lens), "algorithmic_bytes": nbytes,
+                     "us_mean": round(mean * 1e3, 2), "us_median": round(med * 1e3, 2),
+                     "gbps": round(nbytes / (mean * 1e-3) / 1e9, 1),
+                     "pct_of_hbm_peak": round(100 * nbytes / (mean * 1e-3) / 1e9 / HBM_PEAK_GBS, 2),
+                     "calls": calls, "pool_copies_rotated": copies}
+        del ws
+        torch.cuda.empty_cache()
+    return out
+
+
 def main():
     args = parse_args()
     if args.gpus != 1:
@@ -387,6 +574,7 @@ def main():
         raise SystemExit(2)
     import torch
 
+    from engine import workloads
     from engine.kernels.paged_attention import paged_attention_decode_batched
     from engine.kernels.paged_attention_integration import paged_kv_write
 
@@ -395,18 +583,13 @@ def main():
         print(json.dumps({"reference_grid": reference_grid(dev)}), flush=True)
         return
     if args.decode_only:
-        dec = decode_benchmark(dev, args.seed, args.decode_batch, args.decode_steps)
+        model = workloads.decode_model(dev, args.seed)
+        prompts = workloads.decode_prompts(args.seed, args.decode_batch)
+        dec, _, _ = decode_benchmark(dev, model, prompts, args.decode_steps)
         print(json.dumps({"decode_tokens_per_s": dec["tokens_per_s"], "decode": dec}), flush=True)
         return
-    copies = [make_workload(args.workload, dev, args.seed)]
-    base = copies[0]
-    for _ in range(1, max(1, args.copies)):
-        from engine.workloads import Workload
-
-        copies.append(Workload(name=base.name, q=base.q.clone(), k_cache=base.k_cache.clone(),
-                               v_cache=base.v_cache.clone(), block_tables=base.block_tables.clone(),
-                               seq_lens=base.seq_lens.clone(), tables=base.tables, lens=base.lens,
-                               scale=base.scale, unique_slots=base.unique_slots, meta=base.meta))
+    base = make_workload(args.workload, dev, args.seed)
+    copies = [base] + [clone_workload(base) for _ in range(1, max(1, args.copies))]
     g = torch.Generator(device=dev).manual_seed(args.seed + 7)
     hkv, d = base.k_cache.shape[2], base.k_cache.shape[3]
     new_k = torch.randn(base.num_seqs, hkv, d, generator=g, device=dev).half()
@@ -445,11 +628,15 @@ def main():
     attn_ms = [a.elapsed_time(b) for a, b in events]
     attn_mean = statistics.fmean(attn_ms)
     attn_med = statistics.median(attn_ms)
+    # The planned statistic as well: median of 60 attention calls over the rotated copies.
+    med60 = statistics.median(time_calls(copies, 60, warmup=0))
 
     alg_bytes = base.algorithmic_bytes(unique=True)
     logical_bytes = base.algorithmic_bytes(unique=False)
     achieved = alg_bytes / (attn_mean * 1e-3) / 1e9
-    traffic = read_traffic() if args.workload == "long_context" else None
+    traffic, traffic_digest = (read_traffic() if args.workload == "long_context"
+                               else (None, None))
+    digest = source_digest()
 
     result = {
         "metric": "paged-decode attention HBM GB/s (% of peak) + decode tokens/sec, 1 MI355X",
@@ -479,6 +666,8 @@ def main():
         },
         "attention_ms_mean": round(attn_mean, 5),
         "attention_ms_median": round(attn_med, 5),
+        "attention_ms_median_of_60": round(med60, 5),
+        "gbps_median_of_60": round(alg_bytes / (med60 * 1e-3) / 1e9, 2),
         "algorithmic_bytes": alg_bytes,
         "logical_bytes": logical_bytes,
         "pct_of_hbm_peak": round(100 * achieved / HBM_PEAK_GBS, 2),
@@ -488,25 +677,48 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": traffic,
+            # FETCH_SIZE + WRITE_SIZE per launch from the committed rocprofv3 summary, used only
+            # when it was measured on these very sources.
+            "traffic": traffic if traffic_digest == digest else None,
         },
+        "traffic_profile": {"bytes": traffic, "sources_sha256": traffic_digest,
+                            "matches_current_sources": traffic_digest == digest},
+        "sources_sha256": digest,
         "decode_tokens_per_s": None,
     }
+    log(f"headline: {attn_mean * 1e3:.1f} us mean, {achieved:.0f} GB/s")
     result["copy_ceiling_gbps"] = copy_ceiling(dev)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(base, args.cpu_seconds)
+        log(f"cpu baseline: {result['cpu_baseline']['value']} GB/s")
+    del copies, base
+    torch.cuda.empty_cache()
+    if not args.no_configs:
+        result["configs"] = config_timings(dev, args.seed)
+        log("config timings done")
     if not args.no_prefill:
         # A batch of prompt suffixes, and one long prompt the way the reference
         # prefills (one sequence at a time; its key ranges are split).
         result["prefix_prefill"] = prefill_benchmark(dev, args.seed)
         result["prefix_prefill_single"] = prefill_benchmark(dev, args.seed, B=1, cached=8192,
                                                             new=1024)
+        log("prefill attention done")
     if not args.no_decode:
-        del copies, base
+        model = workloads.decode_model(dev, args.seed)
+        prompts = workloads.decode_prompts(args.seed, args.decode_batch)
+        dec, runner, seqs = decode_benchmark(dev, model, prompts, args.decode_steps)
+        log(f"decode: {dec['tokens_per_s']} tokens/s")
+        del runner
         torch.cuda.empty_cache()
-        dec = decode_benchmark(dev, args.seed, args.decode_batch, args.decode_steps)
+        unfused, _, _ = decode_benchmark(dev, model, prompts, args.decode_steps,
+                                         fuse_layers=False, attention_share=False)
+        log(f"decode without fused layers: {unfused['tokens_per_s']} tokens/s")
+        dec["unfused_layers"] = {k: unfused[k] for k in ("tokens_per_s", "ms_per_step",
+                                                         "graphs_captured")}
         result["decode_tokens_per_s"] = dec["tokens_per_s"]
         result["decode"] = dec
+        if not args.no_cpu_baseline:
+            result["cpu_baseline"]["decode_step"] = cpu_decode_steps(model, seqs)
     print(json.dumps(result), flush=True)
 
 

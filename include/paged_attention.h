@@ -51,7 +51,8 @@ enum {
 /* ABI revision of this header; bumps whenever a signature or a workspace
  * contract changes (2: zero-initialised decode workspace; 3: pa_rope_kv_write_f16;
  * 4: pa_prefill_attention_f16; 5: its workspace; 6: pa_rmsnorm_f16, pa_silu_mul_f16;
- * 7: residual input of pa_rmsnorm_f16, pa_top2_f16; 8: pa_linear_f16). */
+ * 7: residual input of pa_rmsnorm_f16, pa_top2_f16; 8: pa_linear_f16; 9: pa_linear_f16
+ * removed, decode workspace sizes stated per current device). */
 PA_API int pa_abi_version(void);
 
 /* Message of the last failed call on this thread ("" after a success). */
@@ -79,7 +80,9 @@ PA_API int pa_decode_batched_f16(const void* q, const int64_t q_strides[3],
                           float scale, void* workspace, size_t workspace_bytes,
                           void* stream);
 
-/* Workspace the call above needs for these sizes (0 is a valid answer). */
+/* Workspace the call above needs for these sizes (0 is a valid answer), on the
+ * current HIP device: the schedule, and so the size, depends on that device's
+ * compute-unit count. Query it with the device of the call current. */
 PA_API size_t pa_decode_batched_workspace_bytes(int num_seqs, int num_q_heads, int num_kv_heads,
                                          int head_dim, int block_size,
                                          int max_blocks_per_seq);
@@ -266,36 +269,6 @@ PA_API int pa_silu_mul_f16(const void* gate_up, int64_t gate_up_row_stride, void
                            int64_t out_row_stride, int rows, int inter, void* stream);
 PA_API int pa_top2_f16(const void* logits, int64_t row_stride, int rows, int vocab,
                        int64_t* index, float* top, void* stream);
-
-/*
- * Linear layers of the decode step. No counterpart in the reference, whose
- * decode step runs transformers' nn.Linear projections through torch
- * (paged_attention_integration.py:103-105 and :175 for attention, the model's
- * MLP for the rest); this replaces them, with the MLP's SwiGLU and the
- * residual adds folded in, for the few rows a decode step has.
- *
- * pa_linear_f16: with X = x [rows, in_features] and W = weight (unit stride
- * along in_features, fp16), accumulating in fp32:
- *   epilogue 0: y = fp16(X W^T + bias)   (W [out_features, in], bias optional)
- *   epilogue 1: y = fp16(y + X W^T)      (in place: torch.addmm_)
- *   epilogue 2: W holds [gate; up] ([2 out_features, in]) and
- *               y = fp16(fp16(silu(fp16(X Wg^T))) * fp16(X Wu^T))
- * in_features must be a multiple of 32 and out_features of 4; x and weight
- * rows 16-byte aligned, y and bias 8-byte aligned; y must not overlap x or W.
- * splits <= 0 chooses how many workgroups share each output tile's K range;
- * when that is more than one the call needs pa_linear_workspace_bytes() of
- * workspace whose first bytes (arrival counters) are zero before the first
- * call and are left zero by every call, so one workspace serves calls in
- * sequence on one stream (calls that overlap must not share it). Results do
- * not depend on which workgroup finishes first.
- */
-PA_API size_t pa_linear_workspace_bytes(int rows, int out_features, int in_features,
-                                        int epilogue, int splits);
-PA_API int pa_linear_f16(const void* x, int64_t x_row_stride, const void* weight,
-                         int64_t weight_row_stride, const void* bias, void* y,
-                         int64_t y_row_stride, int rows, int out_features, int in_features,
-                         int epilogue, int splits, void* workspace, size_t workspace_bytes,
-                         void* stream);
 
 #ifdef __cplusplus
 }

@@ -175,15 +175,32 @@ def test_workload_softmax_stress(cuda_device):
 
 @pytest.mark.parametrize("hkv", [28, 14, 7, 4])
 def test_workload_gqa_sweep(cuda_device, hkv):
+    """Batch 64 x 2048 tokens, 28 q heads, head_dim 128: every sequence against the oracle."""
     w = workloads.gqa_sweep(hkv, device=cuda_device, seed=hkv)
-    _check_workload(w, seqs=[0, 1, 31, 63])
+    _check_workload(w)
 
 
 def test_workload_long_context(cuda_device):
-    """Batch 256 with shared prefixes: one whole prefix group plus the longest sequences."""
+    """The headline shape (batch 256, lognormal lengths to ~19k, groups of 8 sharing prefix
+    blocks): every sequence against the oracle."""
     w = workloads.long_context(device=cuda_device, seed=0)
-    longest = sorted(range(w.num_seqs), key=lambda i: -w.lens[i])[:4]
-    _check_workload(w, seqs=sorted(set(list(range(8)) + longest)))
+    _check_workload(w)
+
+
+def _device_cus(device):
+    return torch.cuda.get_device_properties(device).multi_processor_count
+
+
+@pytest.mark.parametrize("extra", [0, 1])
+def test_decode_step_layer_at_the_head_group_boundary(cuda_device, extra):
+    """One layer's call of the batch-128 decode step (14 q / 2 kv, head_dim 64, lengths
+    64 + U[64, 1024]), every row against the oracle. With sequences x kv heads up to the CU
+    count each (sequence, kv head) pair runs alone on a workgroup; one sequence more and
+    pairs hold both kv heads. Both sides of that boundary are checked: batch CUs/2 (128 on
+    MI355X, the decode step's own schedule) and CUs/2 + 1."""
+    b = _device_cus(cuda_device) // 2 + extra
+    w = workloads.decode_step_layer(b, device=cuda_device, seed=b)
+    _check_workload(w)
 
 
 @pytest.mark.parametrize("d", [32, 64, 128, 256])

@@ -92,20 +92,26 @@ class FakePrefillModel:
         return SimpleNamespace(logits=logits, past_key_values=SimpleNamespace(layers=[layer]))
 
 
-def _runner(model, mode, device):
+def _runner(model, mode, device, debug=False):
     """The fixture model has no attention modules to patch, so "full" mode runs the
     reference's own DynamicCache path (paged_prefill=False), which these fixtures pin."""
     from engine.kernels.paged_attention_integration import KernelPagedManualDecode
 
     return KernelPagedManualDecode(model=model, block_size=2, num_blocks=2, device=str(device),
-                                   dtype=torch.float16, prefix_mode=mode, paged_prefill=False)
+                                   dtype=torch.float16, prefix_mode=mode, paged_prefill=False,
+                                   debug_prefix_cache=debug)
 
 
-def test_prefill_keeps_hit_blocks_and_copies_only_owned_blocks(cuda_device):
-    """Reference fixture :60-91: block 0 is a cache hit and must not be overwritten."""
+def test_prefill_keeps_hit_blocks_and_copies_only_owned_blocks(cuda_device, caplog):
+    """Reference fixture :60-91: block 0 is a cache hit and must not be overwritten; with
+    debug_prefix_cache the cached rows are compared with the fresh prefill and the reference's
+    log line reports no difference (:91)."""
+    import logging
+
     from engine.memory.block_pool import BlockTable
 
-    runner = _runner(FakePrefillModel(cuda_device), "share", cuda_device)
+    caplog.set_level(logging.INFO, logger="engine.kernels.paged_attention_integration")
+    runner = _runner(FakePrefillModel(cuda_device), "share", cuda_device, debug=True)
     for t in runner.pool.k_cache + runner.pool.v_cache:
         t.zero_()
     hit_k = torch.zeros(2, 1, 64, dtype=torch.float16, device=cuda_device)
@@ -123,6 +129,30 @@ def test_prefill_keeps_hit_blocks_and_copies_only_owned_blocks(cuda_device):
     assert k1[:, 0, :2].tolist() == [[2, 3], [3, 4]]
     assert runner.pool.v_cache[0][1].float().cpu()[:, 0, :2].tolist() == [[102, 103], [103, 104]]
     assert seq.last_logit_margin == 1.0
+    assert "layer=0 max_abs_difference=0 (cached_tokens=2)" in caplog.text
+
+
+def test_debug_prefix_cache_reports_the_largest_difference(cuda_device, caplog):
+    """A cached row that differs from the fresh prefill shows up as the logged maximum: the
+    reference's per-token loop (integration.py:328-362) restated as one device reduction."""
+    import logging
+
+    from engine.memory.block_pool import BlockTable
+
+    caplog.set_level(logging.INFO, logger="engine.kernels.paged_attention_integration")
+    runner = _runner(FakePrefillModel(cuda_device), "share", cuda_device, debug=True)
+    for t in runner.pool.k_cache + runner.pool.v_cache:
+        t.zero_()
+    runner.pool.k_cache[0][0, :, 0, :2] = torch.tensor([[0, 1], [1, 2]], dtype=torch.float16)
+    runner.pool.v_cache[0][0, :, 0, :] = 100
+    runner.pool.v_cache[0][0, :, 0, :2] = torch.tensor([[100, 101], [101, 102]], dtype=torch.float16)
+    runner.pool.k_cache[0][0, 1, 0, 5] = 0.75   # key row of token 1 off by 0.75
+    runner.pool.v_cache[0][0, 0, 0, 9] = 100.25  # value row of token 0 off by 0.25
+    table = BlockTable(seq_id=0, block_size=2, physical_block_ids=[0, 1], num_tokens=4)
+    seq = SimpleNamespace(prompt_token_ids=[10, 11, 12, 13], block_table=table, num_cached_tokens=2,
+                          last_logits=None, last_logit_margin=None)
+    runner.prefill(seq)
+    assert "layer=0 max_abs_difference=0.75 (cached_tokens=2)" in caplog.text
 
 
 def test_full_prefill_uses_cached_prefix_and_only_forwards_suffix(cuda_device):

@@ -121,3 +121,55 @@ def test_launch_tensors_must_share_one_device():
     _native.same_device(a, torch.ones(3))
     with pytest.raises(AssertionError, match="same device"):
         _native.same_device(a, b)
+
+
+def test_workspace_is_never_allocated_during_graph_capture(monkeypatch):
+    """A scratch buffer missing or too small while a graph is capturing raises instead of
+    allocating (a fill recorded into the graph, memory from the capture's pool); one that is
+    already large enough is handed out; a grown buffer keeps the old one alive."""
+    from engine.kernels import _native
+
+    dev = torch.device("cpu")  # the allocation itself never happens below
+    key = (dev.index, 0x1234, _native.WS_DECODE)
+    monkeypatch.setattr(_native, "_workspaces", {})
+    monkeypatch.setattr(_native, "_retired", [])
+    monkeypatch.setattr(torch.cuda, "is_current_stream_capturing", lambda: True)
+    with pytest.raises(_native.CaptureAllocationError, match="capturing"):
+        _native.workspace(4096, dev, 0x1234)
+    assert key not in _native._workspaces
+    held = torch.zeros(8192, dtype=torch.uint8)
+    _native._workspaces[key] = held
+    assert _native.workspace(4096, dev, 0x1234) == held.data_ptr()
+    with pytest.raises(_native.CaptureAllocationError):
+        _native.workspace(16384, dev, 0x1234)
+    assert _native._workspaces[key] is held
+    monkeypatch.setattr(torch.cuda, "is_current_stream_capturing", lambda: False)
+    addr = _native.workspace(16384, dev, 0x1234)
+    assert addr != held.data_ptr() and _native._retired == [held]
+    assert _native._workspaces[key].numel() >= 1 << 20 and _native._workspaces[key].sum() == 0
+    assert _native.workspace(0, dev, 0x1234) is None
+
+
+def test_fused_layers_patch_only_when_asked():
+    """Decode contexts bind the fused decoder layer (and the one-launch norm) on prepared
+    layers only with fuse_layers; without it, and for prefill contexts, transformers' layer
+    forwards stay; attention modules are always patched, and everything is restored."""
+    from transformers import Qwen2Config, Qwen2ForCausalLM
+
+    from engine.kernels.paged_attention_integration import (
+        patch_paged_attention, prepare_fused_layers)
+
+    torch.manual_seed(0)
+    model = Qwen2ForCausalLM(Qwen2Config(vocab_size=64, hidden_size=32, intermediate_size=64,
+                                         num_hidden_layers=2, num_attention_heads=4,
+                                         num_key_value_heads=2)).half()
+    assert prepare_fused_layers(model) == 2
+    layer = model.model.layers[0]
+    decode = SimpleNamespace(is_decode=True)
+    prefill = SimpleNamespace(is_decode=False, is_prefill=True)
+    for ctx, fuse, fused in ((decode, True, True), (decode, False, False), (prefill, True, False)):
+        with patch_paged_attention(model, ctx, fuse_layers=fuse):
+            assert ("forward" in vars(layer)) == fused
+            assert ("forward" in vars(layer.input_layernorm)) == fused
+            assert "forward" in vars(layer.self_attn)
+        assert "forward" not in vars(layer) and "forward" not in vars(layer.self_attn)

@@ -48,9 +48,6 @@ HIPCC_FLAGS = [
 # (-fno-honor-nans; infinities, which the masking uses, keep their meaning).
 FILE_FLAGS = {
     "pa_prefill.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1", "-fno-honor-nans"],
-    # The linear layer's 32 accumulators stay in place only in the VGPR form;
-    # in the accumulator-register form they are copied around every product.
-    "pa_linear.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
 }
 
 

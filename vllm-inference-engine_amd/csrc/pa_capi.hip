@@ -260,48 +260,13 @@ static PrefillPlan prefill_plan(int num_seqs, int num_q_heads, int num_kv_heads,
   return p;
 }
 
-// ---- decode-step linear layer: tiles, K splits and workspace ----
-
-// A K split takes at least this many K steps of 32.
-constexpr int kLinMinSteps = 4;
-
-struct LinearPlan {
-  int n_tiles, m_tiles, splits;
-  size_t counter_bytes, part_bytes;
-};
-
-// Output tiles of 16 x kLinearNtw columns (half that for SwiGLU) by 128 rows;
-// K is split (splits <= 0: automatically) until the launch has about one
-// workgroup per CU, each split keeping at least kLinMinSteps K steps.
-static LinearPlan linear_plan(int rows, int out_features, int in_features, int epilogue,
-                              int splits) {
-  LinearPlan p{};
-  const int cols = (epilogue == kLinSwiglu ? 8 : 16) * kLinearNtw;
-  p.n_tiles = (out_features + cols - 1) / cols;
-  p.m_tiles = (rows + 127) / 128;
-  const int tiles = p.n_tiles * p.m_tiles;
-  const int ks = in_features / 32;
-  if (splits <= 0) {
-    splits = (device_cus() + tiles - 1) / tiles;
-    const int cap = ks / kLinMinSteps > 0 ? ks / kLinMinSteps : 1;
-    splits = splits < cap ? splits : cap;
-  }
-  splits = splits < ks ? splits : ks;
-  p.splits = splits < 1 ? 1 : splits;
-  if (p.splits > 1) {
-    p.counter_bytes = ((size_t)tiles * sizeof(int) + 255) & ~(size_t)255;
-    p.part_bytes = (size_t)tiles * p.splits * 2 * kLinearNtw * 256 * 16;
-  }
-  return p;
-}
-
 }  // namespace pa
 
 using namespace pa;
 
 extern "C" {
 
-int pa_abi_version(void) { return 8; }
+int pa_abi_version(void) { return 9; }
 
 const char* pa_last_error(void) { return g_error.c_str(); }
 
@@ -881,86 +846,6 @@ int pa_silu_mul_f16(const void* gate_up, int64_t gate_up_row_stride, void* out,
                    aligned(gate_up, 16) && aligned(out, 16);
   return finish_launch(launch_silu_mul((const f16*)gate_up, gate_up_row_stride, (f16*)out,
                                        out_row_stride, rows, inter, vec, (hipStream_t)stream));
-}
-
-size_t pa_linear_workspace_bytes(int rows, int out_features, int in_features, int epilogue,
-                                 int splits) {
-  if (rows <= 0 || out_features <= 0 || in_features < 32) return 0;
-  const LinearPlan p = linear_plan(rows, out_features, in_features, epilogue, splits);
-  return p.counter_bytes + p.part_bytes;
-}
-
-int pa_linear_f16(const void* x, int64_t x_row_stride, const void* weight,
-                  int64_t weight_row_stride, const void* bias, void* y, int64_t y_row_stride,
-                  int rows, int out_features, int in_features, int epilogue, int splits,
-                  void* workspace, size_t workspace_bytes, void* stream) {
-  clear_error();
-  if (rows < 0 || out_features <= 0 || in_features <= 0) {
-    set_error("rows must be >= 0, out_features and in_features > 0");
-    return PA_ERR_ARG;
-  }
-  if (epilogue != kLinStore && epilogue != kLinAdd && epilogue != kLinSwiglu) {
-    set_error("unknown epilogue %d", epilogue);
-    return PA_ERR_ARG;
-  }
-  if (rows == 0) return PA_OK;
-  if (!x || !weight || !y) {
-    set_error("null pointer argument");
-    return PA_ERR_ARG;
-  }
-  if (bias && epilogue != kLinStore) {
-    set_error("a bias is only taken by the store epilogue");
-    return PA_ERR_ARG;
-  }
-  if (in_features % 32 || out_features % 4) {
-    set_error("in_features must be a multiple of 32 and out_features of 4 (got %d, %d)",
-              in_features, out_features);
-    return PA_ERR_UNSUPPORTED;
-  }
-  if (x_row_stride < in_features || weight_row_stride < in_features ||
-      y_row_stride < out_features) {
-    set_error("row strides must be at least the row lengths");
-    return PA_ERR_ARG;
-  }
-  if (x_row_stride % 8 || weight_row_stride % 8 || y_row_stride % 4 || !aligned(x, 16) ||
-      !aligned(weight, 16) || !aligned(y, 8) || (bias && !aligned(bias, 8))) {
-    set_error("x and weight need 16-byte aligned rows, y and bias 8-byte alignment");
-    return PA_ERR_ARG;
-  }
-  const int64_t w_rows = epilogue == kLinSwiglu ? 2 * (int64_t)out_features : out_features;
-  const int64_t x_bytes = 2 * ((int64_t)(rows - 1) * x_row_stride + in_features);
-  const int64_t w_bytes = 2 * ((w_rows - 1) * weight_row_stride + in_features);
-  const LinearPlan p = linear_plan(rows, out_features, in_features, epilogue, splits);
-  const int64_t grid = (int64_t)p.n_tiles * p.m_tiles * p.splits;
-  if (x_bytes >= ((int64_t)1 << 31) - 16 || w_bytes >= ((int64_t)1 << 31) - 16 ||
-      p.part_bytes >= ((size_t)1 << 31) || grid > 0x7fffffff) {
-    set_error("operands of 2 GiB or more are not supported");
-    return PA_ERR_UNSUPPORTED;
-  }
-  const size_t need = p.counter_bytes + p.part_bytes;
-  if (need && (!workspace || workspace_bytes < need)) {
-    set_error("workspace of %zu bytes needed, %zu given", need, workspace_bytes);
-    return PA_ERR_WORKSPACE;
-  }
-  LinearArgs a{};
-  a.x = (const f16*)x;
-  a.xs = x_row_stride;
-  a.w = (const f16*)weight;
-  a.wsr = weight_row_stride;
-  a.bias = (const f16*)bias;
-  a.y = (f16*)y;
-  a.ys = y_row_stride;
-  a.cnt = need ? (int*)workspace : nullptr;
-  a.part = need ? (float*)((char*)workspace + p.counter_bytes) : nullptr;
-  a.part_bytes = (int)p.part_bytes;
-  a.M = rows;
-  a.N = out_features;
-  a.K = in_features;
-  a.n_tiles = p.n_tiles;
-  a.splits = p.splits;
-  a.x_bytes = (int)x_bytes;
-  a.w_bytes = (int)w_bytes;
-  return finish_launch(launch_linear(a, epilogue, (hipStream_t)stream));
 }
 
 int pa_top2_f16(const void* logits, int64_t row_stride, int rows, int vocab, int64_t* index,

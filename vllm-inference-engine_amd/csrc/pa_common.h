@@ -174,28 +174,6 @@ constexpr size_t kPfCounterBytes = (size_t)kPfMaxCounters * sizeof(int);
 // buffers of 128 keys would leave no LDS for a second workgroup).
 __host__ __device__ constexpr int prefill_key_tile(int D) { return D <= 64 ? 128 : 64; }
 
-// Decode-step linear layer Y = X W^T (pa_linear.hip). Element strides; unit
-// stride along K. Epilogues: see kLin*.
-enum { kLinStore = 0, kLinAdd = 1, kLinSwiglu = 2 };
-// Weight tiles of 16 rows per wavefront: a workgroup covers 16 x kLinearNtw
-// weight rows (output columns; half of them for the SwiGLU epilogue).
-constexpr int kLinearNtw = 4;
-struct LinearArgs {
-  const f16* x;  // [M, K]
-  int64_t xs;
-  const f16* w;  // [N, K]; [2 N, K] for SwiGLU
-  int64_t wsr;
-  const f16* bias;  // [N] or null (kLinStore)
-  f16* y;           // [M, N]
-  int64_t ys;
-  float* part;  // split-K partial tiles
-  int part_bytes;
-  int* cnt;  // per-tile arrival counters, zero between launches
-  int M, N, K;
-  int n_tiles, splits;
-  int x_bytes, w_bytes;  // extents of the operand buffer resources
-};
-
 // Launchers (defined next to their kernels).
 hipError_t launch_decode_split(const DecodeArgs& a, int D, int num_seqs, hipStream_t s);
 hipError_t launch_decode_v1(const DecodeArgs& a, int D, hipStream_t s);
@@ -211,7 +189,6 @@ hipError_t launch_silu_mul(const f16* gu, int64_t gs, f16* out, int64_t os, int 
                            bool vec, hipStream_t s);
 hipError_t launch_top2(const f16* logits, int64_t ls, int rows, int V, int64_t* idx, float* top,
                        bool vec, hipStream_t s);
-hipError_t launch_linear(const LinearArgs& a, int epilogue, hipStream_t s);
 
 // Length of sequence b clamped to [0, max_blocks * bs].
 __device__ inline int clamped_len(const DecodeArgs& a, int b) {

@@ -17,7 +17,7 @@ import torch  # noqa: F401  (must be loaded before the HIP library, see above)
 
 LIB_NAME = "libpa_gfx950.so"
 LIB_PATH = Path(__file__).with_name(LIB_NAME)
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 PA_OK = 0
 PA_ERR_ARG = 1
@@ -66,9 +66,6 @@ SIGNATURES: dict[str, tuple] = {
                                _vp]),
     "pa_top2_f16": (_i32, [_vp, _i64, _i32, _i32, _vp, _vp, _vp]),
     "pa_silu_mul_f16": (_i32, [_vp, _i64, _vp, _i64, _i32, _i32, _vp]),
-    "pa_linear_workspace_bytes": (_sz, [_i32, _i32, _i32, _i32, _i32]),
-    "pa_linear_f16": (_i32, [_vp, _i64, _vp, _i64, _vp, _vp, _i64, _i32, _i32, _i32, _i32, _i32,
-                              _vp, _sz, _vp]),
 }
 
 _lib = None
@@ -142,9 +139,16 @@ WS_SCORES = "scores"
 # "prefill" serves pa_prefill_attention_f16: its counters follow the same
 # zero-between-calls contract as the decode ones, with another layout.
 WS_PREFILL = "prefill"
-# "linear" serves pa_linear_f16: per-tile arrival counters (same contract),
-# then the split-K partial tiles.
-WS_LINEAR = "linear"
+
+
+# Buffers replaced by larger ones. A HIP graph captured with an older buffer's
+# address keeps writing there on every replay, so a replaced buffer is never
+# handed back to the allocator.
+_retired: list[torch.Tensor] = []
+
+
+class CaptureAllocationError(NativeLibraryError):
+    """A scratch buffer would have to be allocated while a HIP graph is being captured."""
 
 
 def workspace(nbytes: int, device: torch.device, stream: int, kind: str = WS_DECODE) -> int | None:
@@ -154,14 +158,28 @@ def workspace(nbytes: int, device: torch.device, stream: int, kind: str = WS_DEC
     one stream is ordered, so a call never overwrites scratch a previous call
     on that stream still reads. Calls on different streams get different
     buffers. Memory comes from torch's caching allocator; a new buffer starts
-    zero-filled (the decode kernels' counters rely on it).
+    zero-filled (the decode kernels' counters rely on it). A buffer that grows
+    is replaced by one of at least twice its size and the old one is kept
+    alive, since graphs captured with it still address it.
+
+    Allocating (and zero-filling) while the current stream is capturing a
+    HIP graph would record a fill into the graph and tie the buffer to the
+    capture's memory pool, so it raises CaptureAllocationError instead: run
+    the captured work once eagerly first, which sizes the buffer.
     """
     if nbytes == 0:
         return None
     key = (device.index, stream, kind)
     buf = _workspaces.get(key)
     if buf is None or buf.numel() < nbytes:
-        buf = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        if torch.cuda.is_current_stream_capturing():
+            raise CaptureAllocationError(
+                f"{kind} workspace of {nbytes} bytes for stream {stream:#x} is not allocated yet "
+                "and the stream is capturing a graph; run the step once before capturing it")
+        size = max(nbytes, 1 << 20, 0 if buf is None else 2 * buf.numel())
+        if buf is not None:
+            _retired.append(buf)
+        buf = torch.zeros(size, dtype=torch.uint8, device=device)
         _workspaces[key] = buf
     return buf.data_ptr()
 

@@ -105,13 +105,15 @@ def paged_attention_decode_batched(
         return out
     max_blocks = block_tables.shape[1]
     lib = _native.load()
-    key = (num_seqs, num_q_heads, num_kv_heads, head_dim, block_size, max_blocks)
-    ws_bytes = _ws_sizes.get(key)
-    if ws_bytes is None:
-        ws_bytes = _ws_sizes[key] = lib.pa_decode_batched_workspace_bytes(*key)
     dev = q.device
+    # The workspace size depends on the device's compute-unit count: keyed by
+    # device and queried with that device current.
+    key = (dev.index, num_seqs, num_q_heads, num_kv_heads, head_dim, block_size, max_blocks)
     stream = _native.stream_handle(dev)
     with _on_device(dev):
+        ws_bytes = _ws_sizes.get(key)
+        if ws_bytes is None:
+            ws_bytes = _ws_sizes[key] = lib.pa_decode_batched_workspace_bytes(*key[1:])
         status = lib.pa_decode_batched_f16(
             q.data_ptr(), _native.strides_of(q),
             k_cache.data_ptr(), _native.strides_of(k_cache),
@@ -177,11 +179,11 @@ def paged_attention_prefill(
     max_blocks = block_tables.shape[1]
     key = ("prefill", num_seqs, num_q_heads, num_kv_heads, head_dim, block_size, max_blocks,
            int(max_query_len), dev.index)
-    ws_bytes = _ws_sizes.get(key)
-    if ws_bytes is None:
-        ws_bytes = _ws_sizes[key] = lib.pa_prefill_attention_workspace_bytes(*key[1:8])
     stream = _native.stream_handle(dev)
     with _on_device(dev):
+        ws_bytes = _ws_sizes.get(key)
+        if ws_bytes is None:
+            ws_bytes = _ws_sizes[key] = lib.pa_prefill_attention_workspace_bytes(*key[1:8])
         status = lib.pa_prefill_attention_f16(
             q.data_ptr(), _native.strides_of(q),
             k_cache.data_ptr(), _native.strides_of(k_cache),
@@ -229,11 +231,11 @@ def _single_seq_call(fn_name, ws_name, q, k_cache, v_cache, block_table, seq_len
     if table_len == 0:
         # Only reachable with seq_len == 0: nothing to attend to.
         return out.zero_()
-    ws_bytes = getattr(lib, ws_name)(num_q_heads, num_kv_heads, head_dim, block_size,
-                                     ws_last(table_len, seq_len))
     dev = q.device
     stream = _native.stream_handle(dev)
     with _on_device(dev):
+        ws_bytes = getattr(lib, ws_name)(num_q_heads, num_kv_heads, head_dim, block_size,
+                                         ws_last(table_len, seq_len))
         status = getattr(lib, fn_name)(
             q.data_ptr(), _native.strides_of(q),
             k_cache.data_ptr(), _native.strides_of(k_cache),

@@ -25,7 +25,9 @@ layer (reference pad + index_copy_, :278-326).
 from __future__ import annotations
 
 import itertools
+import logging
 import math
+from collections import OrderedDict
 from contextlib import contextmanager
 from typing import Any, Callable, List, Optional, Tuple, Union
 
@@ -40,6 +42,8 @@ from .paged_attention import (
     paged_attention_decode_batched,
     paged_attention_prefill,
 )
+
+logger = logging.getLogger(__name__)
 
 __all__ = [
     "PagedAttentionContext",
@@ -468,52 +472,6 @@ def silu_mul(gate_up: torch.Tensor) -> torch.Tensor:
     return out
 
 
-LINEAR_STORE, LINEAR_ADD, LINEAR_SWIGLU = 0, 1, 2
-
-
-def linear(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor] = None, *,
-           out: Optional[torch.Tensor] = None, accumulate: bool = False, swiglu: bool = False,
-           splits: int = 0) -> torch.Tensor:
-    """A decode step's projection x W^T (pa_linear_f16), fp16 rows, fp32 accumulation.
-
-    - default: nn.functional.linear(x, weight, bias);
-    - accumulate: out.addmm_(x, weight.t()) in place (out required);
-    - swiglu: weight is a merged [gate; up] projection [2 N, K] and the result is
-      silu(x Wg^T) * (x Wu^T) [rows, N] with the MLP's fp16 roundings.
-    `splits` forces the number of workgroups sharing each output tile's K range
-    (0: chosen by the library).
-    """
-    assert x.is_cuda and x.dtype == torch.float16 and weight.dtype == torch.float16
-    assert x.dim() == 2 and weight.dim() == 2 and x.stride(1) == 1 and weight.stride(1) == 1
-    assert not (accumulate and swiglu) and (bias is None or not (accumulate or swiglu))
-    rows, k = x.shape
-    n = weight.shape[0] // 2 if swiglu else weight.shape[0]
-    assert weight.shape[1] == k and (not swiglu or weight.shape[0] % 2 == 0)
-    if accumulate:
-        assert out is not None and out.shape == (rows, n) and out.dtype == torch.float16
-        epi = LINEAR_ADD
-    else:
-        epi = LINEAR_SWIGLU if swiglu else LINEAR_STORE
-        if out is None:
-            out = torch.empty(rows, n, dtype=torch.float16, device=x.device)
-    assert out.stride(1) == 1
-    extra = [bias] if bias is not None else []
-    _native.same_device(x, weight, out, *extra)
-    if bias is not None:
-        assert bias.shape == (n,) and bias.dtype == torch.float16
-        bias = bias.contiguous()
-    lib = _native.load()
-    with _on_device(x.device):
-        stream = _native.stream_handle(x.device)
-        nbytes = lib.pa_linear_workspace_bytes(rows, n, k, epi, splits)
-        ws = _native.workspace(nbytes, x.device, stream, _native.WS_LINEAR)
-        status = lib.pa_linear_f16(x.data_ptr(), x.stride(0), weight.data_ptr(), weight.stride(0),
-                                   bias.data_ptr() if bias is not None else None, out.data_ptr(),
-                                   out.stride(0), rows, n, k, epi, splits, ws, nbytes, stream)
-    _native.check(status, "pa_linear_f16")
-    return out
-
-
 def _is_decoder_layer(m: nn.Module) -> bool:
     attn, mlp = getattr(m, "self_attn", None), getattr(m, "mlp", None)
     return (attn is not None and mlp is not None
@@ -619,16 +577,19 @@ def _fused_rms_norm_forward(self: nn.Module, hidden_states: torch.Tensor) -> tor
 
 
 @contextmanager
-def patch_paged_attention(model: nn.Module, context: PagedAttentionContext):
+def patch_paged_attention(model: nn.Module, context: PagedAttentionContext,
+                          fuse_layers: bool = True):
     """Temporarily bind paged_decode_attention_forward on every attention module (reference :179-208).
 
-    For a decode context, decoder layers prepared by prepare_fused_layers()
-    also get fused_decoder_layer_forward, and RMSNorm modules (those with
-    `weight` and `variance_epsilon`) the one-launch norm, for the same
-    duration; prefill contexts keep transformers' layers and norms.
+    For a decode context with fuse_layers, decoder layers prepared by
+    prepare_fused_layers() also get fused_decoder_layer_forward, and RMSNorm
+    modules (those with `weight` and `variance_epsilon`) the one-launch norm,
+    for the same duration; prefill contexts, and decode contexts without
+    fuse_layers, keep transformers' layers and norms.
     """
     patched: List[Tuple[nn.Module, Callable, str]] = []
-    decode = getattr(context, "is_decode", False) and not getattr(context, "is_prefill", False)
+    decode = (fuse_layers and getattr(context, "is_decode", False)
+              and not getattr(context, "is_prefill", False))
     for module in model.modules():
         if all(hasattr(module, n) for n in ("q_proj", "k_proj", "v_proj", "o_proj")):
             orig_fwd = module.forward
@@ -653,7 +614,14 @@ def patch_paged_attention(model: nn.Module, context: PagedAttentionContext):
         yield context
     finally:
         for module, orig_fwd, kind in patched:
-            module.forward = orig_fwd
+            # A forward bound on the instance before patching is put back; otherwise the
+            # class's forward shows through again (no instance attribute is left behind).
+            if getattr(orig_fwd, "__self__", None) is module and \
+                    getattr(orig_fwd, "__func__", None) is getattr(type(module).forward, "__func__",
+                                                               type(module).forward):
+                del module.forward
+            else:
+                module.forward = orig_fwd
             for attr in ("_orig_attention_forward", "_paged_attention_context",
                          "_orig_layer_forward", "_orig_norm_forward"):
                 if hasattr(module, attr):
@@ -699,27 +667,47 @@ def paged_prefill_copy(
     _native.check(status, "pa_prefill_copy_f16")
 
 
+def graph_batch_size(n: int) -> int:
+    """Batch size of the captured graph that serves a step of n sequences.
+
+    Steps replay a graph captured for the smallest bucket that holds the
+    batch: 1, 2, 4, 8, then multiples of 16 up to 256, then multiples of 64.
+    The rows past n are padding: length 0, which the K/V write skips and the
+    attention kernel answers with a zero row, and their logits are dropped.
+    Padding costs little (the projections are bound by their weights, not
+    their rows), and a scheduler whose batch changes every step reuses a few
+    graphs instead of capturing one per size.
+    """
+    assert n >= 1
+    if n <= 8:
+        return 1 << (n - 1).bit_length()
+    if n <= 256:
+        return -(-n // 16) * 16
+    return -(-n // 64) * 64
+
+
 class _DecodeGraph:
-    """One decode step captured as a HIP graph for a fixed batch size and table width.
+    """One decode step captured as a HIP graph for a batch-size bucket and table width.
 
     Static device buffers hold the step's inputs: token ids and lengths (one
     pinned host-to-device copy per step, unpacked inside the graph) and the
     zero-padded block tables (copied only when a row changed: a sequence
-    gained a block or the batch was reordered). The graph replays the whole
-    model forward -- each layer's fused RoPE + K/V write and paged attention
-    included -- so a step costs one replay instead of a few hundred kernel
-    launches from Python. The greedy token and top-1/top-2 margin are computed
-    after the replay, outside the graph: top-k and arg-max over a full
-    vocabulary row use multi-block reductions whose scratch is cleared with
-    memset operations, which are not captured into the graph. The capture runs
-    on the graph's own stream, so the decode workspace its kernels use is its
-    own.
+    gained a block or the batch was reordered). Rows past the step's batch are
+    padding with length 0. The graph replays the whole model forward -- each
+    layer's fused RoPE + K/V write and paged attention included -- so a step
+    costs one replay instead of a few hundred kernel launches from Python.
+    The greedy token and top-1/top-2 margin are computed after the replay,
+    outside the graph: top-k and arg-max over a full vocabulary row use
+    multi-block reductions whose scratch is cleared with memset operations,
+    which are not captured into the graph. Every graph of a runner is
+    captured on the runner's one capture stream into one shared memory pool:
+    replays run one at a time on the current stream, and each graph's output
+    buffer stays alive with it.
     """
 
     def __init__(self, runner: "KernelPagedManualDecode", batch: int, width: int):
         dev = runner.device
         self.batch, self.width = batch, width
-        self.stream = torch.cuda.Stream(dev)
         self.host_in = torch.zeros(2, batch, dtype=torch.long).pin_memory()  # ids, lengths
         self.dev_in = torch.zeros(2, batch, dtype=torch.long, device=dev)
         self.host_tables = torch.zeros(batch, width, dtype=torch.int32).pin_memory()
@@ -733,25 +721,31 @@ class _DecodeGraph:
         self.runner = runner
         self.graph: Optional[torch.cuda.CUDAGraph] = None
         self.logits: Optional[torch.Tensor] = None
+        self.rows = 0
 
     def _body(self):
         self.ids.copy_(self.dev_in[0].view(-1, 1))
         self.lens.copy_(self.dev_in[1])
-        self.pos.copy_((self.dev_in[1] - 1).view(-1, 1))
+        self.pos.copy_((self.dev_in[1] - 1).clamp_min(0).view(-1, 1))  # padding rows: position 0
         model = self.runner.model
-        with patch_paged_attention(model, self.ctx):
+        with patch_paged_attention(model, self.ctx, fuse_layers=self.runner.fuse_layers):
             out = model(input_ids=self.ids, position_ids=self.pos, use_cache=False)
         return out.logits[:, -1, :]
 
     def load(self, tokens: List[int], lens: List[int], rows: List[List[int]]) -> None:
         """Stage this step's inputs (asynchronous copies on the current stream)."""
+        n = len(tokens)
+        assert n <= self.batch
+        self.rows = n
         hin = self.host_in.numpy()
-        hin[0] = tokens
-        hin[1] = lens
+        hin[:, n:] = 0
+        hin[0, :n] = tokens
+        hin[1, :n] = lens
         self.dev_in.copy_(self.host_in, non_blocking=True)
         # One vectorised scatter of all rows (a Python loop over 128 rows of
         # numpy slice assignments costs about 0.1 ms per step).
-        counts = np.fromiter((len(r) for r in rows), dtype=np.int64, count=len(rows))
+        counts = np.zeros(self.batch, dtype=np.int64)
+        counts[:n] = np.fromiter((len(r) for r in rows), dtype=np.int64, count=n)
         flat = np.fromiter(itertools.chain.from_iterable(rows), dtype=np.int32,
                            count=int(counts.sum()))
         table = np.zeros((self.batch, self.width), dtype=np.int32)
@@ -762,19 +756,22 @@ class _DecodeGraph:
             self.mirror = table
 
     def run(self) -> torch.Tensor:
-        """Replays the step (capturing it on first use); returns the last-position logits."""
+        """Replays the step (capturing it on first use); returns the batch's last-position logits."""
         if self.graph is None:
-            cur = torch.cuda.current_stream(self.runner.device)
-            self.stream.wait_stream(cur)
-            with torch.cuda.stream(self.stream):
+            runner = self.runner
+            stream = runner._capture_stream()
+            cur = torch.cuda.current_stream(runner.device)
+            stream.wait_stream(cur)
+            with torch.cuda.stream(stream):
                 for _ in range(2):  # warm-up: libraries pick kernels, scratch is allocated
                     self._body()
-            cur.wait_stream(self.stream)
+            cur.wait_stream(stream)
             self.graph = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(self.graph, stream=self.stream):
+            with torch.cuda.graph(self.graph, pool=runner._graph_pool, stream=stream):
                 self.logits = self._body()
+            runner.graph_captures += 1
         self.graph.replay()
-        return self.logits
+        return self.logits[:self.rows]
 
 
 def _seq_field(seq, name, default=None):
@@ -802,8 +799,13 @@ class KernelPagedManualDecode:
     batched forward with paged_decode_attention_forward patched into every
     attention module, so each layer runs the fused RoPE + K/V write and the
     batched paged attention kernel. With use_graphs (the default) the forward
-    is captured once per (batch size, table width) as a HIP graph over
-    persistent device tables and lengths, and each step replays it. The step
+    is captured once per (batch-size bucket, table width) as a HIP graph over
+    persistent device tables and lengths (graph_batch_size: the rows past the
+    batch are zero-length padding), and each step replays it; at most
+    max_graphs graphs are kept, sharing one capture stream and memory pool,
+    so a batch that changes every step, as under continuous batching
+    (reference engine/scheduler/continuous_batching.py:337-476), reuses a
+    bounded set of graphs. The step
     makes one device-to-host transfer (tokens and top-1/top-2 margins
     together) instead of the reference's per-sequence logits copies
     (:643-651); `last_logits` stays on the device.
@@ -823,6 +825,7 @@ class KernelPagedManualDecode:
         use_graphs: bool = True,
         paged_prefill: bool = True,
         fuse_layers: bool = True,
+        max_graphs: int = 32,
     ):
         from ..memory.block_pool import FreeListAllocator, PhysicalBlockPool
 
@@ -851,10 +854,16 @@ class KernelPagedManualDecode:
                                       head_dim=self.head_dim, dtype=dtype, device=self.device)
         self.allocator = FreeListAllocator(num_blocks)
         self._grad_probed = False
-        # Batched decode steps replay captured HIP graphs, one per (batch size,
-        # table width rounded up to a multiple of 64 blocks).
+        # Batched decode steps replay captured HIP graphs, one per (batch-size
+        # bucket, table width rounded up to a multiple of 64 blocks), at most
+        # max_graphs of them (least recently used dropped first), all captured
+        # on one stream into one memory pool.
         self.use_graphs = use_graphs
-        self._graphs: dict = {}
+        self.max_graphs = max(1, int(max_graphs))
+        self._graphs: "OrderedDict[tuple, _DecodeGraph]" = OrderedDict()
+        self._graph_stream: Optional[torch.cuda.Stream] = None
+        self._graph_pool = None
+        self.graph_captures = 0
         # "full" prefix mode: forward the suffix through the paged prefill
         # kernel over the pool (True) or, as the reference does, through
         # transformers' attention over a DynamicCache copy of the prefix.
@@ -865,6 +874,23 @@ class KernelPagedManualDecode:
         self.fuse_layers = fuse_layers and dtype == torch.float16
         if self.fuse_layers:
             prepare_fused_layers(model)
+
+    def _capture_stream(self) -> torch.cuda.Stream:
+        if self._graph_stream is None:
+            self._graph_stream = torch.cuda.Stream(self.device)
+            self._graph_pool = torch.cuda.graph_pool_handle()
+        return self._graph_stream
+
+    def _decode_graph(self, n: int, width: int) -> _DecodeGraph:
+        key = (graph_batch_size(n), width)
+        graph = self._graphs.get(key)
+        if graph is None:
+            graph = self._graphs[key] = _DecodeGraph(self, *key)
+            while len(self._graphs) > self.max_graphs:
+                self._graphs.popitem(last=False)
+        else:
+            self._graphs.move_to_end(key)
+        return graph
 
     # -- prefill -----------------------------------------------------------------
     def _copy_prefill_kv(self, pkv: Any, block_table: Any, prompt_len: int, skip_blocks: int = 0) -> None:
@@ -886,6 +912,36 @@ class KernelPagedManualDecode:
             v_src = values[0, :, start_token:prompt_len, :].permute(1, 0, 2)
             paged_prefill_copy(k_src, v_src, self.pool.k_cache[layer_idx],
                                self.pool.v_cache[layer_idx], ids, prompt_len - start_token)
+
+    def _compare_cached_prefill_kv(self, pkv: Any, block_table: Any, cached_tokens: int) -> None:
+        """Log, per layer, how far the pool's cached prefix rows are from a fresh prefill's K/V.
+
+        The reference's debug_prefix_cache diagnostic (integration.py:328-362,
+        called at :490-491): the largest |fresh - stored| over the cached
+        tokens' keys and values, compared in fp32 after casting the fresh rows
+        to the pool dtype, logged as "Prefix-cache KV comparison layer=%d
+        max_abs_difference=%g (cached_tokens=%d)". Here every layer's maximum
+        is formed on the device and all of them come back in one transfer.
+        """
+        nb = cached_tokens // self.block_size
+        ids = torch.tensor(block_table.physical_block_ids[:nb], dtype=torch.long, device=self.device)
+        worst = []
+        for layer_idx in range(self.num_layers):
+            if hasattr(pkv, "layers"):
+                keys, values = pkv.layers[layer_idx].keys, pkv.layers[layer_idx].values
+            else:
+                keys, values = pkv[layer_idx][0], pkv[layer_idx][1]
+            diffs = []
+            for fresh, pool in ((keys, self.pool.k_cache[layer_idx]),
+                                (values, self.pool.v_cache[layer_idx])):
+                # [1, Hkv, T, D] -> [cached, Hkv, D]; pool rows of the cached blocks, in order.
+                f = fresh[0, :, :cached_tokens, :].permute(1, 0, 2).to(self.dtype).float()
+                st = pool.index_select(0, ids).flatten(0, 1)[:cached_tokens].float()
+                diffs.append((f - st).abs().amax())
+            worst.append(torch.stack(diffs).amax())
+        for layer_idx, diff in enumerate(torch.stack(worst).tolist()):
+            logger.info("Prefix-cache KV comparison layer=%d max_abs_difference=%g "
+                        "(cached_tokens=%d)", layer_idx, diff, cached_tokens)
 
     def _build_cached_prefix(self, block_table: Any, cached_tokens: int):
         """DynamicCache holding the cached prefix blocks (reference :364-392)."""
@@ -945,6 +1001,8 @@ class KernelPagedManualDecode:
                     logits_to_keep=1)
             else:
                 out = self.model(input_ids=input_ids, use_cache=True, logits_to_keep=1)
+                if self.debug_prefix_cache and cached:
+                    self._compare_cached_prefill_kv(out.past_key_values, block_table, cached)
             self._copy_prefill_kv(out.past_key_values, block_table, prompt_len,
                                   skip_blocks=cached // self.block_size)
         logits = out.logits[:, -1, :]
@@ -995,9 +1053,7 @@ class KernelPagedManualDecode:
         if self.use_graphs:
             rows = [bt.physical_block_ids for bt in tables]
             width = max(64, -(-max(len(r) for r in rows) // 64) * 64)
-            graph = self._graphs.get((n, width))
-            if graph is None:
-                graph = self._graphs[(n, width)] = _DecodeGraph(self, n, width)
+            graph = self._decode_graph(n, width)
             graph.load(last_tokens, seq_lens, rows)
             logits = graph.run().clone()  # the graph's output buffer is reused by the next step
         else:
@@ -1005,7 +1061,7 @@ class KernelPagedManualDecode:
             position_ids = torch.tensor([[L - 1] for L in seq_lens], dtype=torch.long,
                                         device=self.device)
             ctx = PagedAttentionContext(self.pool, tables, seq_lens, self.block_size, True)
-            with patch_paged_attention(self.model, ctx):
+            with patch_paged_attention(self.model, ctx, fuse_layers=self.fuse_layers):
                 out = self.model(input_ids=input_ids, position_ids=position_ids, use_cache=False)
             logits = out.logits[:, -1, :]
         if logits.dtype == torch.float16 and logits.stride(-1) == 1:
@@ -1057,7 +1113,7 @@ class KernelPagedManualDecode:
             block_table.num_tokens += 1
             ctx = PagedAttentionContext(self.pool, [block_table], [seq_len], self.block_size, True)
             pos = torch.tensor([[seq_len - 1]], dtype=torch.long, device=self.device)
-            with patch_paged_attention(self.model, ctx):
+            with patch_paged_attention(self.model, ctx, fuse_layers=self.fuse_layers):
                 step = self.model(input_ids=next_token, position_ids=pos, use_cache=False)
             logits = step.logits[:, -1, :]
             history.append(logits)

@@ -165,6 +165,43 @@ def long_context(device="cpu", seed=0, num_seqs=256, sigma=0.5, group=8,
                    meta={"sigma": sigma, "group": group, "prefix_blocks": prefix_blocks})
 
 
+def decode_step_layer(num_seqs=128, device="cpu", seed=0) -> Workload:
+    """One layer's attention call in the middle of the batch-128 decode step.
+
+    Qwen2.5-0.5B heads (14 q / 2 kv, head_dim 64), block 16; lengths are the
+    decode-step workload's prompts, U[64, 1024], plus 64 generated tokens.
+    """
+    rng = np.random.default_rng(seed)
+    lens = (rng.integers(64, 1025, size=num_seqs) + 64).tolist()
+    return make_random(num_seqs, 14, 2, 64, lens, 16, seed=seed, device=device,
+                       name=f"decode_step_layer_b{num_seqs}")
+
+
+# Qwen2.5-0.5B architecture: 24 layers, hidden 896, 14 q / 2 kv heads (head_dim
+# 64), SwiGLU MLP 4864, RMSNorm eps 1e-6, RoPE theta 1e6, vocabulary 151936;
+# the lm_head is not tied to the embeddings (transformers' Qwen2Config default).
+QWEN25_05B = dict(vocab_size=151936, hidden_size=896, intermediate_size=4864, num_hidden_layers=24,
+                  num_attention_heads=14, num_key_value_heads=2, max_position_embeddings=32768,
+                  rope_theta=1e6, rms_norm_eps=1e-6, tie_word_embeddings=False)
+
+
+def decode_model(device, seed=0, config=None):
+    """Random-init (transformers' N(0, 0.02)) Qwen2 causal LM in fp16, eval mode."""
+    from transformers import Qwen2Config, Qwen2ForCausalLM
+
+    torch.manual_seed(seed)
+    with torch.device(device):
+        model = Qwen2ForCausalLM(Qwen2Config(**(config or QWEN25_05B)))
+    return model.half().eval()
+
+
+def decode_prompts(seed=0, batch=128, vocab=QWEN25_05B["vocab_size"]) -> list:
+    """The decode-step workload's prompts: lengths U[64, 1024], random token ids."""
+    rng = np.random.default_rng(seed)
+    lens = rng.integers(64, 1025, size=batch)
+    return [rng.integers(0, vocab, size=int(n)).tolist() for n in lens]
+
+
 def gather_subset(w: Workload, seqs: list[int]) -> tuple:
     """Copy the blocks the given sequences read to the CPU with a compact table.
 
