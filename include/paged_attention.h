@@ -52,7 +52,8 @@ enum {
  * contract changes (2: zero-initialised decode workspace; 3: pa_rope_kv_write_f16;
  * 4: pa_prefill_attention_f16; 5: its workspace; 6: pa_rmsnorm_f16, pa_silu_mul_f16;
  * 7: residual input of pa_rmsnorm_f16, pa_top2_f16; 8: pa_linear_f16; 9: pa_linear_f16
- * removed, decode workspace sizes stated per current device). */
+ * removed, decode workspace sizes stated per current device; 10:
+ * pa_decode_batched_noalloc_f16). */
 PA_API int pa_abi_version(void);
 
 /* Message of the last failed call on this thread ("" after a success). */
@@ -269,6 +270,33 @@ PA_API int pa_silu_mul_f16(const void* gate_up, int64_t gate_up_row_stride, void
                            int64_t out_row_stride, int rows, int inter, void* stream);
 PA_API int pa_top2_f16(const void* logits, int64_t row_stride, int rows, int vocab,
                        int64_t* index, float* top, void* stream);
+
+/*
+ * Batched decode attention that allocates nothing. No counterpart in the
+ * reference; it is for callers that cannot allocate device memory or hand
+ * over a workspace: code under HIP graph capture, tight serving loops,
+ * harnesses that forbid allocation. Same arguments, kernels and results (the
+ * same bits) as pa_decode_batched_f16, without the workspace: the split-K
+ * scratch lives in a fixed array of PA_NOALLOC_SCRATCH_BYTES that the library
+ * holds on each GPU it runs on until the process ends. Calls whose scratch
+ * need exceeds it, and batches beyond the stream-K plan (more than 1024
+ * sequences or 65536 sequence x kv-head-group pairs), are refused with
+ * PA_ERR_UNSUPPORTED before any launch. Every call on one GPU uses that GPU's
+ * one array: calls that overlap in time on one GPU (concurrent streams or
+ * threads) race and must not be made; calls ordered on one stream are fine.
+ * The first call on a device also launches a small fill kernel, on the call's
+ * stream, that clears the array's counters.
+ */
+#define PA_NOALLOC_SCRATCH_BYTES ((size_t)16 << 20)
+PA_API int pa_decode_batched_noalloc_f16(const void* q, const int64_t q_strides[3],
+                                         const void* k_cache, const int64_t k_strides[4],
+                                         const void* v_cache, const int64_t v_strides[4],
+                                         const int32_t* block_tables, const int64_t bt_strides[2],
+                                         const int32_t* seq_lens, void* out,
+                                         const int64_t out_strides[3], int num_seqs,
+                                         int num_q_heads, int num_kv_heads, int head_dim,
+                                         int block_size, int num_blocks, int max_blocks_per_seq,
+                                         float scale, void* stream);
 
 #ifdef __cplusplus
 }

@@ -161,3 +161,16 @@ def test_error_text_is_thread_local():
     t.join()
     assert seen["msg"] == b""
     assert b"head_dim" in lib.pa_last_error()
+
+
+def test_noalloc_entry_refuses_what_its_scratch_cannot_hold():
+    """The no-allocation entry point checks its limits on the host, before any launch."""
+    lib = _native.load()
+    args = (16, _strides(896, 64, 1), 16, _strides(2048, 128, 64, 1), 16,
+            _strides(2048, 128, 64, 1), 16, _strides(64, 1), 16, 16, _strides(896, 64, 1))
+    rc = lib.pa_decode_batched_noalloc_f16(*args, 1100, 14, 2, 64, 16, 100, 64, 0.125, None)
+    assert rc == _native.PA_ERR_UNSUPPORTED
+    assert b"no-allocation" in lib.pa_last_error() and b"1024" in lib.pa_last_error()
+    assert lib.pa_decode_batched_noalloc_f16(*args, 4, 14, 2, 48, 16, 100, 64, 0.125, None) == \
+        _native.PA_ERR_UNSUPPORTED  # head_dim outside the built set, as for the workspace entry
+

@@ -171,10 +171,9 @@ static int device_cus() {
   return n;
 }
 
-// Fills the stream-K fields of `a` and launches; `ws` holds the pair counters
-// then the records.
-static hipError_t launch_streamk_with(DecodeArgs& a, int num_seqs, int head_dim, void* ws,
-                                      hipStream_t s) {
+// Fills the stream-K schedule fields of `a` (head group, grid, ranges) for a
+// launch over num_seqs sequences; the workspace pointers are set at launch.
+static void streamk_plan(DecodeArgs& a, int num_seqs, int head_dim) {
   const int bound = streamk_grid_bound(num_seqs, a.hkv, head_dim, a.bs, a.max_blocks);
   const int want = kSkWgPerCu * device_cus();
   a.num_seqs = num_seqs;
@@ -196,9 +195,24 @@ static hipError_t launch_streamk_with(DecodeArgs& a, int num_seqs, int head_dim,
   const int tile_bytes = 64 * a.head_group * head_dim;
   a.seg_cost = (240 << 10) / tile_bytes;
   a.min_range = kSkMinRange;
+}
+
+// Workspace bytes the planned launch touches: the pair counters, then two
+// partial records per workgroup of its grid (at most what
+// streamk_workspace() reserves for the same sizes).
+static size_t streamk_need(const DecodeArgs& a, int head_dim) {
+  return kSkCounterBytes +
+         (size_t)a.num_wg * 2 * a.head_group * record_floats(head_dim) * sizeof(float);
+}
+
+// Launches a planned stream-K call; `ws` holds the pair counters then the
+// records, ws_bytes of them (at least streamk_need()).
+static hipError_t launch_streamk_planned(DecodeArgs& a, int head_dim, void* ws, size_t ws_bytes,
+                                         hipStream_t s) {
   a.cnt = (int*)ws;
   a.recs = (float*)((char*)ws + kSkCounterBytes);
-  a.recs_bytes = (int)streamk_records_bytes(num_seqs, a.hkv, head_dim, bound);
+  const size_t rb = ws_bytes - kSkCounterBytes;
+  a.recs_bytes = rb < 0x7fffffffu ? (int)rb : 0x7fffffff;
   return launch_decode_streamk(a, head_dim, s);
 }
 
@@ -266,7 +280,7 @@ using namespace pa;
 
 extern "C" {
 
-int pa_abi_version(void) { return 9; }
+int pa_abi_version(void) { return 10; }
 
 const char* pa_last_error(void) { return g_error.c_str(); }
 
@@ -295,6 +309,23 @@ int pa_decode_batched_f16(const void* q, const int64_t q_strides[3], const void*
                           int max_blocks_per_seq, float scale, void* workspace,
                           size_t workspace_bytes, void* stream) {
   clear_error();
+  return pa::decode_batched(q, q_strides, k_cache, k_strides, v_cache, v_strides, block_tables,
+                            bt_strides, seq_lens, out, out_strides, num_seqs, num_q_heads,
+                            num_kv_heads, head_dim, block_size, num_blocks, max_blocks_per_seq,
+                            scale, workspace, workspace_bytes, nullptr, stream);
+}
+
+}  // extern "C"
+
+namespace pa {
+
+int decode_batched(const void* q, const int64_t q_strides[3], const void* k_cache,
+                   const int64_t k_strides[4], const void* v_cache, const int64_t v_strides[4],
+                   const int32_t* block_tables, const int64_t bt_strides[2],
+                   const int32_t* seq_lens, void* out, const int64_t out_strides[3],
+                   int num_seqs, int num_q_heads, int num_kv_heads, int head_dim,
+                   int block_size, int num_blocks, int max_blocks_per_seq, float scale,
+                   void* workspace, size_t workspace_bytes, ScratchFn scratch, void* stream) {
   if (num_seqs < 0) {
     set_error("num_seqs must be >= 0");
     return PA_ERR_ARG;
@@ -323,11 +354,12 @@ int pa_decode_batched_f16(const void* q, const int64_t q_strides[3], const void*
   }
   const int st = split_tiles_for(kSplitTilesBatched, block_size);
   const int64_t ms = splits_for(max_tiles_for(max_blocks_per_seq, block_size), st);
-  const size_t need = pa_decode_batched_workspace_bytes(num_seqs, num_q_heads, num_kv_heads,
-                                                        head_dim, block_size, max_blocks_per_seq);
-  if (need && (!workspace || workspace_bytes < need)) {
-    set_error("workspace of %zu bytes needed, %zu given", need, workspace_bytes);
-    return PA_ERR_WORKSPACE;
+  const bool streamk = streamk_ok(num_seqs, num_kv_heads, head_dim);
+  if (scratch && !streamk) {
+    set_error("the no-allocation entry point takes at most %d sequences and %d (sequence, "
+              "kv-head group) pairs; %d sequences of %d kv heads given",
+              kSkMaxSeqs, kSkMaxPairs, num_seqs, num_kv_heads);
+    return PA_ERR_UNSUPPORTED;
   }
   DecodeArgs a{};
   a.q = (const f16*)q;
@@ -358,10 +390,39 @@ int pa_decode_batched_f16(const void* q, const int64_t q_strides[3], const void*
   a.split_tiles = st;
   a.max_splits = (int)ms;
   a.scale_log2 = scale * kLog2e;
-  if (streamk_ok(num_seqs, num_kv_heads, head_dim))
-    return finish_launch(launch_streamk_with(a, num_seqs, head_dim, workspace, (hipStream_t)stream));
-  return finish_launch(launch_decode_split(a, head_dim, num_seqs, (hipStream_t)stream));
+  if (!streamk) {
+    const size_t need = pa_decode_batched_workspace_bytes(num_seqs, num_q_heads, num_kv_heads,
+                                                          head_dim, block_size, max_blocks_per_seq);
+    if (need && (!workspace || workspace_bytes < need)) {
+      set_error("workspace of %zu bytes needed, %zu given", need, workspace_bytes);
+      return PA_ERR_WORKSPACE;
+    }
+    return finish_launch(launch_decode_split(a, head_dim, num_seqs, (hipStream_t)stream));
+  }
+  streamk_plan(a, num_seqs, head_dim);
+  const size_t need = streamk_need(a, head_dim);
+  if (scratch) {
+    // The caller cannot allocate: the library's own fixed buffer, if it is large enough.
+    if (need > workspace_bytes) {
+      set_error("this call needs %zu bytes of scratch; the no-allocation entry point has %zu",
+                need, workspace_bytes);
+      return PA_ERR_UNSUPPORTED;
+    }
+    const int rc = scratch(&workspace, (hipStream_t)stream);
+    if (rc) return rc;
+  } else if (!workspace || workspace_bytes < need) {
+    const size_t reserve = pa_decode_batched_workspace_bytes(
+        num_seqs, num_q_heads, num_kv_heads, head_dim, block_size, max_blocks_per_seq);
+    set_error("workspace of %zu bytes needed, %zu given", reserve, workspace_bytes);
+    return PA_ERR_WORKSPACE;
+  }
+  return finish_launch(launch_streamk_planned(a, head_dim, workspace, workspace_bytes,
+                                              (hipStream_t)stream));
 }
+
+}  // namespace pa
+
+extern "C" {
 
 // Shared by the single-sequence entry points.
 static int fill_single(DecodeArgs& a, const void* q, const int64_t q_strides[2],
@@ -440,13 +501,15 @@ int pa_decode_v2_f16(const void* q, const int64_t q_strides[2], const void* k_ca
                        bt_stride, table_len, seq_len, out, out_strides, num_q_heads, num_kv_heads,
                        head_dim, block_size, num_blocks, scale);
   if (rc) return rc;
-  const size_t need =
-      pa_decode_v2_workspace_bytes(num_q_heads, num_kv_heads, head_dim, block_size, table_len);
-  if (need && (!workspace || workspace_bytes < need)) {
-    set_error("workspace of %zu bytes needed, %zu given", need, workspace_bytes);
+  streamk_plan(a, 1, head_dim);
+  if (!workspace || workspace_bytes < streamk_need(a, head_dim)) {
+    const size_t reserve =
+        pa_decode_v2_workspace_bytes(num_q_heads, num_kv_heads, head_dim, block_size, table_len);
+    set_error("workspace of %zu bytes needed, %zu given", reserve, workspace_bytes);
     return PA_ERR_WORKSPACE;
   }
-  return finish_launch(launch_streamk_with(a, 1, head_dim, workspace, (hipStream_t)stream));
+  return finish_launch(launch_streamk_planned(a, head_dim, workspace, workspace_bytes,
+                                              (hipStream_t)stream));
 }
 
 size_t pa_decode_v1_workspace_bytes(int num_q_heads, int num_kv_heads, int head_dim,

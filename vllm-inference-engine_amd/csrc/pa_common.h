@@ -174,6 +174,23 @@ constexpr size_t kPfCounterBytes = (size_t)kPfMaxCounters * sizeof(int);
 // buffers of 128 keys would leave no LDS for a second workgroup).
 __host__ __device__ constexpr int prefill_key_tile(int D) { return D <= 64 ? 128 : 64; }
 
+// Supplies the device address of a caller-less scratch buffer for the launch
+// on `stream` (the no-allocation entry point's static array); returns a PA_*
+// status.
+typedef int (*ScratchFn)(void** ptr, hipStream_t stream);
+
+// Batched decode attention behind pa_decode_batched_f16 (pa_capi.hip). With
+// `scratch` set, the workspace is not the caller's: workspace_bytes is the
+// size of the buffer `scratch` supplies, and calls that need more than that,
+// or the fixed-split path, are refused.
+int decode_batched(const void* q, const int64_t q_strides[3], const void* k_cache,
+                   const int64_t k_strides[4], const void* v_cache, const int64_t v_strides[4],
+                   const int32_t* block_tables, const int64_t bt_strides[2],
+                   const int32_t* seq_lens, void* out, const int64_t out_strides[3],
+                   int num_seqs, int num_q_heads, int num_kv_heads, int head_dim,
+                   int block_size, int num_blocks, int max_blocks_per_seq, float scale,
+                   void* workspace, size_t workspace_bytes, ScratchFn scratch, void* stream);
+
 // Launchers (defined next to their kernels).
 hipError_t launch_decode_split(const DecodeArgs& a, int D, int num_seqs, hipStream_t s);
 hipError_t launch_decode_v1(const DecodeArgs& a, int D, hipStream_t s);
