@@ -47,26 +47,46 @@ def _device_cus():
 
 def test_workspace_sizes():
     lib = _native.load()
+    cus = _device_cus()
     rec = (32 + 16 * 64) * 4
     counters = 65536 * 4  # per-pair arrival counters at the start of every decode workspace
-    # Stream-K (<= 1024 sequences): the counters, then 2 records per workgroup of the
-    # grid bound, each covering the kv heads of one pair (1, or 2 at head_dim 64 when
-    # the batch's pairs outnumber the CUs). The bound is the tile count when that is
-    # smaller: 8 sequences x 2 kv heads x 32 tiles here.
-    assert lib.pa_decode_batched_workspace_bytes(8, 14, 2, 64, 16, 32) == counters + 512 * 2 * rec
-    assert lib.pa_decode_batched_workspace_bytes(256, 14, 2, 64, 16, 2048) == counters + 1024 * 2 * 2 * rec
+
+    def streamk(seqs, kv_heads, grid, pair_heads, share):
+        # Two record slots per workgroup of the grid; a slot holds one record per kv head of
+        # a pair, or, where prefix items may be built (head_dim <= 64, block 16 or 32, 64 or
+        # more sequences), one per column block of a prefix item (4). Prefix items add a
+        # suffix and a prefix record per (sequence, kv head).
+        slot = max(pair_heads, 4) if share else pair_heads
+        return counters + grid * 2 * slot * rec + (2 * seqs * kv_heads * rec if share else 0)
+
+    # Stream-K (<= 1024 sequences): the grid is one workgroup per CU, or the tile count
+    # when that is smaller (8 sequences x 2 kv heads x 32 tiles = 512 here).
+    assert lib.pa_decode_batched_workspace_bytes(8, 14, 2, 64, 16, 32) == \
+        streamk(8, 2, min(cus, 512), 1, False)
+    assert lib.pa_decode_batched_workspace_bytes(64, 14, 2, 64, 16, 32) == \
+        streamk(64, 2, min(cus, 4096), 1, True)
+    assert lib.pa_decode_batched_workspace_bytes(256, 14, 2, 64, 16, 2048) == \
+        streamk(256, 2, cus, 2 if 256 * 2 > cus else 1, True)
     rec128 = (32 + 16 * 128) * 4
-    assert lib.pa_decode_batched_workspace_bytes(64, 28, 7, 128, 16, 128) == counters + 1024 * 2 * rec128
+    assert lib.pa_decode_batched_workspace_bytes(64, 28, 7, 128, 16, 128) == \
+        counters + cus * 2 * rec128
+    # Block size 8 never shares prefixes.
+    assert lib.pa_decode_batched_workspace_bytes(64, 14, 2, 64, 8, 64) == \
+        streamk(64, 2, min(cus, 4096), 1, False)
+    # One sequence (the single-sequence entry points) has nothing to share.
+    assert lib.pa_decode_batched_workspace_bytes(1, 14, 2, 64, 16, 2048) == \
+        streamk(1, 2, min(cus, 256), 1, False)
     # Fixed-split path beyond 1024 sequences: 2048-block rows -> 64 splits of 512 tokens,
     # placed after the counter region so one buffer serves both paths.
     assert lib.pa_decode_batched_workspace_bytes(2000, 14, 2, 64, 16, 2048) == counters + 2000 * 2 * 64 * rec
     assert lib.pa_decode_batched_workspace_bytes(2000, 14, 2, 64, 16, 32) == 0
     # kv heads per pair: one while sequences x kv heads stay within the current device's CU
-    # count (256 when no GPU is visible, as on an MI355X), two above it (records hold both heads)
-    half = _device_cus() // 2
-    assert lib.pa_decode_batched_workspace_bytes(half, 14, 2, 64, 16, 2048) == counters + 1024 * 2 * rec
+    # count (256 when no GPU is visible, as on an MI355X), two above it
+    half = cus // 2
+    assert lib.pa_decode_batched_workspace_bytes(half, 14, 2, 64, 16, 2048) == \
+        streamk(half, 2, cus, 1, True)
     assert lib.pa_decode_batched_workspace_bytes(half + 1, 14, 2, 64, 16, 2048) == \
-        counters + 1024 * 2 * 2 * rec
+        streamk(half + 1, 2, cus, 2, True)
     assert lib.pa_decode_v1_workspace_bytes(14, 2, 64, 16, 67) == 2 * 16 * 80 * 4
     assert lib.pa_decode_batched_workspace_bytes(8, 14, 2, 48, 16, 2048) == 0  # unsupported dim
     # Prefill: one sequence, 512 new tokens of 2560. Two column groups per wavefront would give

@@ -124,17 +124,43 @@ static int streamk_grid_bound(int num_seqs, int num_kv_heads, int head_dim, int 
   return (int)(tiles < kSkMaxWG ? (tiles < 1 ? 1 : tiles) : kSkMaxWG);
 }
 
-static size_t streamk_records_bytes(int num_seqs, int num_kv_heads, int head_dim, int grid) {
-  const int hg = streamk_head_group(num_kv_heads, head_dim, num_seqs);
-  return (size_t)grid * 2 * hg * record_floats(head_dim) * sizeof(float);
+// Fewest sequences for which a launch looks for shared prefixes: finding the
+// groups costs every workgroup about 2-3 us at the start of the launch
+// (measured on MI355X), which only large batches recover.
+constexpr int kShareMinSeqs = 64;
+
+// Whether a launch over these sizes may build prefix items: head_dim <= 64,
+// block size 16 or 32, at least kShareMinSeqs sequences (and, at launch, pool
+// strides that the block-size-specialised kernels address; see
+// streamk_can_share).
+static bool streamk_may_share(int num_seqs, int head_dim, int block_size) {
+  return num_seqs >= kShareMinSeqs && head_dim <= 64 && (block_size == 16 || block_size == 32);
+}
+
+// Partial records of a launch of `grid` workgroups: two slots per workgroup of
+// slot_recs records each, plus, with prefix items, one suffix and one prefix
+// record per (sequence, kv head).
+static size_t streamk_records_bytes(int num_seqs, int num_kv_heads, int head_dim, int grid,
+                                    int slot_recs, bool share) {
+  const size_t rec = (size_t)record_floats(head_dim) * sizeof(float);
+  return (size_t)grid * 2 * slot_recs * rec +
+         (share ? (size_t)2 * num_seqs * num_kv_heads * rec : 0);
 }
 
 // Stream-K workspace: the pair counters (kSkCounterBytes, zero between
-// launches) followed by the partial records.
+// launches) followed by the partial records of the largest grid a launch over
+// these sizes uses on the current device, with room for prefix items whenever
+// the sizes allow them.
 static size_t streamk_workspace(int num_seqs, int num_kv_heads, int head_dim, int block_size,
                                 int max_blocks) {
-  const int grid = streamk_grid_bound(num_seqs, num_kv_heads, head_dim, block_size, max_blocks);
-  return kSkCounterBytes + streamk_records_bytes(num_seqs, num_kv_heads, head_dim, grid);
+  const int bound = streamk_grid_bound(num_seqs, num_kv_heads, head_dim, block_size, max_blocks);
+  const int want = kSkWgPerCu * device_cus();
+  const int grid = want < bound ? want : bound;  // the largest grid streamk_plan chooses
+  const int hg = streamk_head_group(num_kv_heads, head_dim, num_seqs);
+  const bool share = streamk_may_share(num_seqs, head_dim, block_size);
+  const int slot_recs = share && kPfxColBlocks > hg ? kPfxColBlocks : hg;
+  return kSkCounterBytes +
+         streamk_records_bytes(num_seqs, num_kv_heads, head_dim, grid, slot_recs, share);
 }
 
 // The stream-K plan holds up to kSkMaxSeqs sequences in LDS and counts
@@ -195,14 +221,20 @@ static void streamk_plan(DecodeArgs& a, int num_seqs, int head_dim) {
   const int tile_bytes = 64 * a.head_group * head_dim;
   a.seg_cost = (240 << 10) / tile_bytes;
   a.min_range = kSkMinRange;
+  // Prefix items: only where ranges are used (one workgroup per pair cuts
+  // nothing and merges nothing) and the kernel builds them.
+  a.max_members = pfx_members(a.g);
+  a.share = !a.pair_per_wg && streamk_may_share(num_seqs, head_dim, a.bs) &&
+            streamk_can_share(a, head_dim);
+  a.slot_recs = a.share && kPfxColBlocks > a.head_group ? kPfxColBlocks : a.head_group;
 }
 
 // Workspace bytes the planned launch touches: the pair counters, then two
 // partial records per workgroup of its grid (at most what
 // streamk_workspace() reserves for the same sizes).
 static size_t streamk_need(const DecodeArgs& a, int head_dim) {
-  return kSkCounterBytes +
-         (size_t)a.num_wg * 2 * a.head_group * record_floats(head_dim) * sizeof(float);
+  return kSkCounterBytes + streamk_records_bytes(a.num_seqs, a.hkv, head_dim, a.num_wg,
+                                                 a.slot_recs, a.share != 0);
 }
 
 // Launches a planned stream-K call; `ws` holds the pair counters then the
@@ -400,7 +432,14 @@ int decode_batched(const void* q, const int64_t q_strides[3], const void* k_cach
     return finish_launch(launch_decode_split(a, head_dim, num_seqs, (hipStream_t)stream));
   }
   streamk_plan(a, num_seqs, head_dim);
-  const size_t need = streamk_need(a, head_dim);
+  size_t need = streamk_need(a, head_dim);
+  if (scratch && need > workspace_bytes && a.share) {
+    // The fixed buffer cannot hold the prefix items' records: read shared
+    // prefixes once per sequence instead.
+    a.share = 0;
+    a.slot_recs = a.head_group;
+    need = streamk_need(a, head_dim);
+  }
   if (scratch) {
     // The caller cannot allocate: the library's own fixed buffer, if it is large enough.
     if (need > workspace_bytes) {

@@ -57,7 +57,26 @@ struct DecodeArgs {
   // little work uses fewer ranges than workgroups (the rest exit at once).
   int min_range;
   int head_group;  // kv heads per stream-K pair (1 or 2)
+  // Shared prefixes (block size a multiple of 16, head_dim <= 64): nonzero
+  // lets the kernel find runs of neighbouring sequences whose leading table
+  // entries are the same physical blocks and read those blocks once per run.
+  int share;
+  int max_members;  // sequences per sharing group (at most kPfxMaxMembers)
+  int slot_recs;    // records per partial-record slot: max(head_group, kPfxColBlocks) when sharing
 };
+
+// Shared-prefix groups: leading table entries compared per sequence, most
+// sequences per group, and column blocks of 16 query rows a prefix item's
+// wavefront computes (the group's members times the query group size).
+constexpr int kPfxCapBlocks = 64;
+constexpr int kPfxMaxMembers = 8;
+constexpr int kPfxColBlocks = 4;
+
+// Members a sharing group may have at query group size g: whole members per
+// 16-column block times the column blocks, at most kPfxMaxMembers.
+__host__ __device__ constexpr int pfx_members(int g) {
+  return (16 / g) * kPfxColBlocks < kPfxMaxMembers ? (16 / g) * kPfxColBlocks : kPfxMaxMembers;
+}
 
 // Stream-K limits: sequences whose tile prefix fits the LDS plan, the largest
 // persistent grid the workspace is sized for, and the (sequence, kv-head
@@ -198,6 +217,9 @@ hipError_t launch_kv_write(const KVWriteArgs& a, bool vec, hipStream_t s);
 hipError_t launch_prefill_copy(const PrefillCopyArgs& a, bool vec, hipStream_t s);
 hipError_t launch_rope_kv_write(const RopeKVArgs& a, bool vec, hipStream_t s);
 hipError_t launch_decode_streamk(const DecodeArgs& a, int D, hipStream_t s);
+// Whether the stream-K kernel launched for `a` builds prefix items (block size
+// 16 or 32, head_dim <= 64, pool strides its tile addressing covers).
+bool streamk_can_share(const DecodeArgs& a, int D);
 hipError_t launch_prefill_attn(const PrefillAttnArgs& a, int D, hipStream_t s);
 hipError_t launch_rmsnorm(const f16* x, int64_t xs, const f16* res, int64_t rs, f16* sum,
                           int64_t ss, const f16* w, f16* y, int64_t ys, int rows, int H,

@@ -1,21 +1,34 @@
 // Stream-K paged decode attention for gfx950 (MI355X).
 //
-// Schedule. The work is the list of (sequence, kv-head group) pairs, each a
-// run of 16-token tiles; the list is ordered sequence-major. A persistent grid
+// Schedule. The work is a sequence-major list of items, each a run of 16-token
+// tiles plus a fixed overhead: the (sequence, kv-head group) pairs, and, where
+// neighbouring sequences share leading blocks, one prefix item per (sharing
+// group, kv head) placed before the group's first sequence. A persistent grid
 // of G workgroups (one per CU, eight wavefronts each) splits the concatenated
-// tile list into G equal contiguous ranges, so every workgroup streams the
-// same number of bytes however skewed the sequence lengths are. Every
-// workgroup derives the plan itself: its threads load the lengths, scan the
-// per-sequence tile counts into LDS and binary-search their range's first pair.
+// list into G equal contiguous ranges, so every workgroup streams the same
+// number of bytes however skewed the sequence lengths are. Every workgroup
+// derives the plan itself: its threads load the lengths, find the sharing
+// groups, scan the per-sequence widths into LDS and binary-search their
+// range's first item.
 //
-// Within a range the workgroup walks pair segments. Wavefront w takes chunks
+// Shared prefixes. Sequence b joins the group of sequence b - 1 when their
+// first table entries are the same physical blocks (up to kPfxCapBlocks
+// entries and both sequences' full blocks are compared); a group holds at
+// most pfx_members(g) sequences and its shared tiles are the fewest any
+// member shares with its predecessor. Its prefix item reads those tiles once
+// per kv head and computes the scores of all members' query heads from them
+// (four 16-column MFMA blocks), leaving one partial record per member; each
+// member's own pairs then cover only the tiles after the prefix. The member's
+// output is the log-sum-exp merge of its prefix and suffix records.
+//
+// Within a range the workgroup walks item segments. Wavefront w takes chunks
 // (NT tiles) w, w + 8, w + 16, ... of the segment, keeping an online softmax
 // per query head, and the eight wavefronts merge their states through LDS in
 // a fixed order at the end of the segment, so results are the same bits on
-// every run. A pair wholly inside the range is written as final fp16 output;
-// a pair cut by a range boundary leaves an fp32 partial record (at most two
-// per workgroup), and the last workgroup to count an arrival for such a pair
-// combines its records by log-sum-exp, in record order.
+// every run. A pair wholly inside the range whose sequence shares no prefix is
+// written as final fp16 output; every other segment leaves fp32 partial
+// records, and the last workgroup to count an arrival for a pair combines the
+// pair's records by log-sum-exp, in a fixed order.
 //
 // Per tile a wavefront loads the K and V rows of HG adjacent kv heads with
 // whole-cache-line, non-temporal 16-byte loads (whole contiguous token rows
@@ -29,6 +42,19 @@
 namespace pa {
 
 using namespace tiles;
+
+// A wavefront-uniform value, moved to a scalar register.
+__device__ inline int uni(int v) { return __builtin_amdgcn_readfirstlane(v); }
+
+// The lane index, computed where it is read and opaque to the compiler: the
+// per-lane values a branch derives from it are then formed inside that branch
+// instead of being hoisted out of the segment loop and kept live (in vector
+// registers) through the other branches' streaming loops.
+__device__ inline int fresh_lane() {
+  int l = __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+  asm volatile("" : "+v"(l));
+  return l;
+}
 
 // First workgroup whose range contains tile x of a T-tile list split G ways.
 __host__ __device__ inline int wg_of(int64_t x, int64_t T, int G) {
@@ -72,15 +98,25 @@ __device__ inline int block_excl_sum(int (&v)[PER], int* s_tot, int lane, int wa
   return total;
 }
 
-template <int D, int NT, int BS, int HG, int NW>
-__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
-void decode_streamk_kernel(DecodeArgs a) {
+// One wavefront's share of an item segment: tiles s0 .. s1 - 1 (token rows
+// 16 ti .. 16 ti + 15 of the sequence whose table row is btrow, length L) of
+// kv heads h0 .. h0 + HGL - 1, in chunks of NTL tiles w, w + NW, ... (w the
+// wavefront). Column block cb of the 16 x 16 score tiles multiplies the query
+// fragments qf[cb] with the K rows of kv head h0 + cb, or of kv head h0 for
+// every block when SHARED_K (a prefix item: all blocks belong to one kv head).
+// Only the first ncb blocks are computed (wavefront-uniform). The online
+// softmax state (exp2 domain) accumulates into m_run, l_run and acc.
+template <int D, int BS, int HGL, int NCB, int NTL, bool SHARED_K, int NW>
+__device__ __forceinline__ void stream_tiles(const DecodeArgs& a, const int32_t* btrow, int h0,
+                                             int s0, int s1, int L, int ncb,
+                                             const f16x8 (&qf)[NCB][D / 32], f16* kst, f16* vst,
+                                             int wave, int lane, float (&m_run)[NCB],
+                                             float (&l_run)[NCB], f32x4 (&acc)[NCB][D / 16]) {
   constexpr int NC = D / 32;
   constexpr int ND = D / 16;
   constexpr int LS = D + 8;
-  constexpr int NTHR = 64 * NW;
-  constexpr int CPR = HG * D / 8;          // 16-byte chunks per token row of a head group
-  constexpr int NI = 16 * CPR / 64;        // load instructions per tile, for K and for V
+  constexpr int CPR = HGL * D / 8;  // 16-byte chunks per token row of the loaded heads
+  constexpr int NI = 16 * CPR / 64;  // load instructions per tile, for K and for V
   // A 16-token tile lies inside one block when 16 divides the block size: its
   // block id and row base are then wavefront-uniform.
   constexpr bool UNIFORM_TILE = BS > 0 && BS % 16 == 0;
@@ -88,16 +124,360 @@ void decode_streamk_kernel(DecodeArgs a) {
   constexpr int RS = 64 / CPR;                // token rows one load instruction covers
   static_assert(NI * 64 == 16 * CPR, "tile must split into whole 64-lane loads");
   static_assert(RS * CPR == 64, "a load instruction must cover whole rows");
+  static_assert(SHARED_K || NCB == HGL, "one column block per loaded kv head");
+  const int row = lane & 15;
+  const int grp = lane >> 4;
+  const int bs = BS > 0 ? BS : a.bs;
+  const int tok_fallback = s0 * 16;  // a valid token of this segment
+
+  // Byte offset of this lane's 16-byte piece within a tile, relative to the
+  // tile's first row at the first loaded kv head (same for every tile).
+  uint32_t k_lane = 0, v_lane = 0;
+  if constexpr (UNIFORM_TILE) {
+    const int lrow = lane / CPR, lcol = (lane % CPR) * 8;
+    const int lhg = lcol / D, ld0 = lcol - lhg * D;
+    k_lane = (uint32_t)(2 * (lrow * a.k_st + lhg * a.k_sh + ld0));
+    v_lane = (uint32_t)(2 * (lrow * a.v_st + lhg * a.v_sh + ld0));
+  }
+
+  // Natural-layout loads: instruction i of a tile gives lane l the 16-byte
+  // chunk f = 64 i + l of the tile's 16 rows x (HGL * D) halves, i.e. row
+  // f / CPR, halves (f % CPR) * 8 of the row's head-group slice. Each
+  // instruction thus reads whole row slices (whole cache lines).
+  auto nat_row = [&](int i) { return (64 * i + lane) / CPR; };
+  auto nat_col = [&](int i) { return ((64 * i + lane) % CPR) * 8; };
+  auto row_token = [&](int ti, int r) {
+    const int t = ti * 16 + r;
+    return (ti < s1 && t < L) ? t : tok_fallback;
+  };
+  auto load_ids = [&](int k, int (&ids)[NTL][NID]) {
+#pragma unroll
+    for (int nt = 0; nt < NTL; ++nt)
+#pragma unroll
+      for (int j = 0; j < NID; ++j) {
+        // A uniform tile lies in one block; otherwise each lane looks up the
+        // block of its own row (also when one instruction covers the tile).
+        const int t = row_token(s0 + k * NTL + nt, UNIFORM_TILE ? 0 : nat_row(j));
+        if constexpr (UNIFORM_TILE)
+          ids[nt][j] = load_uniform(btrow + (int64_t)blk_of<BS>(t, bs) * a.bt_sk);
+        else
+          ids[nt][j] = btrow[(int64_t)blk_of<BS>(t, bs) * a.bt_sk];
+      }
+  };
+  auto load_kv = [&](int k, const int (&ids)[NTL][NID], u32x4 (&kb)[NTL][NI],
+                     u32x4 (&vb)[NTL][NI]) {
+#pragma unroll
+    for (int nt = 0; nt < NTL; ++nt) {
+      const int ti = s0 + k * NTL + nt;
+      if constexpr (UNIFORM_TILE) {
+        // Unconditional: a tile past the segment gets an empty resource.
+        const int64_t id = min(max(ids[nt][0], 0), a.num_blocks - 1);
+        const int64_t r0 = (ti * 16) % BS;
+        const int nb = ti < s1 ? 0x7fffffff : 0;
+        const auto kr = tile_rsrc(a.k + id * a.k_sb + r0 * a.k_st + (int64_t)h0 * a.k_sh, nb);
+        const auto vr = tile_rsrc(a.v + id * a.v_sb + r0 * a.v_st + (int64_t)h0 * a.v_sh, nb);
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+          kb[nt][i] = load_tile(kr, k_lane, (int)(2 * i * RS * a.k_st));
+          vb[nt][i] = load_tile(vr, v_lane, (int)(2 * i * RS * a.v_st));
+        }
+      } else if (ti < s1) {
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+          const int t = row_token(ti, nat_row(i));
+          const int64_t id = min(max(ids[nt][i], 0), a.num_blocks - 1);
+          const int64_t off = off_of<BS>(t, bs);
+          const int col = nat_col(i);
+          const int hg = col / D;
+          const int d0 = col - hg * D;
+          kb[nt][i] = load_stream(a.k + id * a.k_sb + off * a.k_st + (int64_t)(h0 + hg) * a.k_sh + d0);
+          vb[nt][i] = load_stream(a.v + id * a.v_sb + off * a.v_st + (int64_t)(h0 + hg) * a.v_sh + d0);
+        }
+      }
+    }
+  };
+  // Writes one tile's rows (natural layout) into the staging buffer laid out
+  // [tile][head][row][LS]; rows past the sequence end are zeroed when asked.
+  auto stage = [&](int k, u32x4 (&buf)[NTL][NI], f16* dst, bool zero_tail) {
+#pragma unroll
+    for (int nt = 0; nt < NTL; ++nt) {
+      const int ti = s0 + k * NTL + nt;
+      if (ti < s1) {
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+          const int r = nat_row(i);
+          const int col = nat_col(i);
+          const int hg = col / D;
+          const int d0 = col - hg * D;
+          *reinterpret_cast<u32x4*>(&dst[((nt * HGL + hg) * 16 + r) * LS + d0]) = buf[nt][i];
+        }
+        // Rows past the sequence end are overwritten with zeros in LDS (not
+        // selected in registers: a select on freshly loaded registers makes
+        // the compiler wait for those loads where it places the select).
+        if (zero_tail && ti * 16 + 16 > L) {  // wavefront-uniform: the last tile only
+#pragma unroll
+          for (int i = 0; i < NI; ++i) {
+            const int r = nat_row(i);
+            const int col = nat_col(i);
+            const int hg = col / D;
+            const int d0 = col - hg * D;
+            if (ti * 16 + r >= L)
+              *reinterpret_cast<f16x8*>(&dst[((nt * HGL + hg) * 16 + r) * LS + d0]) = zero8();
+          }
+        }
+      }
+    }
+  };
+
+  // Both K and V of chunk k go to LDS first, which frees their registers for
+  // the loads of the chunk two steps ahead; the math then reads LDS only.
+  auto stage_both = [&](int k, u32x4 (&kb)[NTL][NI], u32x4 (&vb)[NTL][NI]) {
+    stage(k, kb, kst, false);
+    stage(k, vb, vst, true);  // V rows past the sequence end as zeros: 0 * garbage is never NaN
+    wave_lds_fence();
+  };
+  auto compute = [&](int k) {
+    float xs[NTL][NCB][4];
+    float mloc[NCB];
+#pragma unroll
+    for (int cb = 0; cb < NCB; ++cb) mloc[cb] = kNegInf;
+#pragma unroll
+    for (int nt = 0; nt < NTL; ++nt) {
+      const int ti = s0 + k * NTL + nt;
+#pragma unroll
+      for (int cb = 0; cb < NCB; ++cb) {
+        if (ti < s1 && cb < ncb) {
+          const int kh = SHARED_K ? 0 : cb;
+          const f16* kt = kst + ((nt * HGL + kh) * 16 + row) * LS + grp * 8;
+          f32x4 s = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int c = 0; c < NC; ++c)
+            s = __builtin_amdgcn_mfma_f32_16x16x32_f16(*reinterpret_cast<const f16x8*>(kt + 32 * c),
+                                                       qf[cb][c], s, 0, 0, 0);
+          if (ti * 16 + 16 <= L) {  // wavefront-uniform: only the last tile is partial
+#pragma unroll
+            for (int r = 0; r < 4; ++r) xs[nt][cb][r] = s[r] * a.scale_log2;
+          } else {
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              xs[nt][cb][r] = ti * 16 + grp * 4 + r < L ? s[r] * a.scale_log2 : kNegInf;
+          }
+#pragma unroll
+          for (int r = 0; r < 4; ++r) mloc[cb] = fmaxf(mloc[cb], xs[nt][cb][r]);
+        } else {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) xs[nt][cb][r] = kNegInf;
+        }
+      }
+    }
+#pragma unroll
+    for (int cb = 0; cb < NCB; ++cb) {
+      if (cb < ncb) {
+        float m = mloc[cb];
+        m = fmaxf(m, __shfl_xor(m, 16));
+        m = fmaxf(m, __shfl_xor(m, 32));
+        const float m_new = fmaxf(m_run[cb], m);
+        const float alpha = fast_exp2(m_run[cb] - m_new);
+        l_run[cb] *= alpha;
+#pragma unroll
+        for (int i = 0; i < ND; ++i) acc[cb][i] *= alpha;
+        m_run[cb] = m_new;
+      }
+    }
+    // Probabilities in fp16 high and remainder parts, then O^T += V^T P^T.
+    auto probs = [&](int nt, int cb, f16x4& ph, f16x4& pl) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float pr = fast_exp2(xs[nt][cb][r] - m_run[cb]);
+        l_run[cb] += pr;
+        const f16 hi = (f16)pr;
+        ph[r] = hi;
+        pl[r] = (f16)(pr - (float)hi);
+      }
+    };
+#pragma unroll
+    for (int nt = 0; nt < NTL; ++nt) {
+      const int ti = s0 + k * NTL + nt;
+      if (ti < s1) {
+        // V^T operand: lane (row, grp) needs V[4 grp + r][16 nd + row], r = 0..3,
+        // which one transposing read of rows 4 grp..4 grp+3 delivers.
+        const f16* vt = vst + (nt * HGL * 16 + grp * 4 + (row >> 2)) * LS + (row & 3) * 4;
+        if constexpr (SHARED_K) {
+          // One V tile for every column block: each transposed read feeds all of them.
+          f16x4 ph[NCB], pl[NCB];
+#pragma unroll
+          for (int cb = 0; cb < NCB; ++cb)
+            if (cb < ncb) probs(nt, cb, ph[cb], pl[cb]);
+#pragma unroll
+          for (int nd = 0; nd < ND; ++nd) {
+            const f16x4 av = lds_read_tr16(vt + nd * 16);
+#pragma unroll
+            for (int cb = 0; cb < NCB; ++cb) {
+              if (cb < ncb) {
+                acc[cb][nd] = __builtin_amdgcn_mfma_f32_16x16x16f16(av, ph[cb], acc[cb][nd], 0, 0, 0);
+                acc[cb][nd] = __builtin_amdgcn_mfma_f32_16x16x16f16(av, pl[cb], acc[cb][nd], 0, 0, 0);
+              }
+            }
+          }
+        } else {
+#pragma unroll
+          for (int cb = 0; cb < NCB; ++cb) {
+            f16x4 ph, pl;
+            probs(nt, cb, ph, pl);
+#pragma unroll
+            for (int nd = 0; nd < ND; ++nd) {
+              const f16x4 av = lds_read_tr16(vt + cb * 16 * LS + nd * 16);
+              acc[cb][nd] = __builtin_amdgcn_mfma_f32_16x16x16f16(av, ph, acc[cb][nd], 0, 0, 0);
+              acc[cb][nd] = __builtin_amdgcn_mfma_f32_16x16x16f16(av, pl, acc[cb][nd], 0, 0, 0);
+            }
+          }
+        }
+      }
+    }
+    wave_lds_fence();
+  };
+
+  // Wavefront-local pipeline over this wavefront's chunks: wavefront w takes
+  // chunks w, w + NW, w + 2 NW, ... A fixed assignment (rather than claims
+  // from a shared counter, which let faster wavefronts take more chunks) keeps
+  // the summation order, and so the result bits, the same on every run; it
+  // costs about 1% at large batches. Step s computes chunk c_s: K/V register
+  // sets Y0/Y1 hold steps s and s+1, id sets X0/X1 the block ids of steps s+2
+  // and s+3. At step s: stage Y[s%2] into LDS, reuse it for the loads of step
+  // s+2 (ids in X[s%2]), claim step s+3 and fetch its ids into X[(s+1)%2],
+  // then compute step s. Claims are increasing per wavefront, so the first
+  // claim past the end ends its work; loads of such chunks are issued anyway
+  // (empty resources, clamped table reads) so that no branch separates them.
+  const int nck = __builtin_amdgcn_readfirstlane((s1 - s0 + NTL - 1) / NTL);
+  int next_chunk = wave;
+  auto claim = [&]() {
+    const int c = next_chunk;
+    next_chunk += NW;
+    return c;
+  };
+  u32x4 kb0[NTL][NI], vb0[NTL][NI], kb1[NTL][NI], vb1[NTL][NI];
+  int ids0[NTL][NID], ids1[NTL][NID];
+  int c0 = claim();
+  int c1 = claim();
+  int c2 = claim();
+  load_ids(c0, ids0);
+  load_ids(c1, ids1);
+  // The scheduler must keep the loads of step 0 ahead of those of step 1:
+  // the loop's waits count on the older buffer being the one staged first.
+  load_kv(c0, ids0, kb0, vb0);
+  __builtin_amdgcn_sched_barrier(0);
+  load_kv(c1, ids1, kb1, vb1);
+  __builtin_amdgcn_sched_barrier(0);
+  load_ids(c2, ids0);
+  // Two steps per trip, one exit: both steps issue their loads on every trip
+  // and only the LDS staging and the math of a step past the end are skipped,
+  // so every path through the loop issues the same loads.
+  while (c0 < nck) {
+    stage_both(c0, kb0, vb0);
+    load_kv(c2, ids0, kb0, vb0);
+    const int c3 = claim();
+    load_ids(c3, ids1);
+    compute(c0);
+    const bool more = c1 < nck;
+    if (more) stage_both(c1, kb1, vb1);
+    load_kv(c3, ids1, kb1, vb1);
+    const int c4 = claim();
+    load_ids(c4, ids0);
+    if (more) compute(c1);
+    c0 = c2;
+    c1 = c3;
+    c2 = c4;
+  }
+}
+
+// Merges the eight wavefronts' states of a segment through LDS (each
+// wavefront's area at smem + w * wave_bytes) and hands every merged output
+// piece to out(cb, nd, M, den, num): for lane (row, grp), column row of
+// column block cb, head_dim elements 16 nd + 4 grp .. + 3, the maximum (exp2
+// domain), the denominator and the four unnormalised accumulators. Every
+// wavefront stores its maxima and denominators per column block and its
+// accumulators in register layout (chunk j = cb * ND + nd: one f32x4 per
+// lane, so the 16-byte LDS writes are conflict-free); wavefront w then
+// combines chunks j = w, w + NW, ... of all wavefronts, in wavefront order.
+template <int D, int NCB, int NW, typename Out>
+__device__ __forceinline__ void merge_waves(char* smem, int wave_bytes, int wave, int lane,
+                                            const float (&m_run)[NCB], const float (&l_run)[NCB],
+                                            const f32x4 (&acc)[NCB][D / 16], int ncb, Out out) {
+  constexpr int ND = D / 16;
+  const int row = lane & 15;
+  const int grp = lane >> 4;
+  float* cm = reinterpret_cast<float*>(smem + wave * wave_bytes);
+  __syncthreads();  // every wavefront is done with its staging buffers
+#pragma unroll
+  for (int cb = 0; cb < NCB; ++cb) {
+    if (cb < ncb) {
+      float l = l_run[cb];
+      l += __shfl_xor(l, 16);
+      l += __shfl_xor(l, 32);
+      if (grp == 0) {
+        cm[cb * 16 + row] = m_run[cb];
+        cm[NCB * 16 + cb * 16 + row] = l;
+      }
+#pragma unroll
+      for (int nd = 0; nd < ND; ++nd)
+        *reinterpret_cast<f32x4*>(&cm[32 * NCB + ((cb * ND + nd) * 64 + lane) * 4]) = acc[cb][nd];
+    }
+  }
+  __syncthreads();
+  for (int j = wave; j < ncb * ND; j += NW) {
+    const int cb = j / ND;
+    const int nd = j - cb * ND;
+    float mw[NW];
+    float M = kNegInf;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      mw[w] = reinterpret_cast<const float*>(smem + w * wave_bytes)[cb * 16 + row];
+      M = fmaxf(M, mw[w]);
+    }
+    float den = 0.f;
+    f32x4 num = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      const float* c = reinterpret_cast<const float*>(smem + w * wave_bytes);
+      const float sc = mw[w] == kNegInf ? 0.f : fast_exp2(mw[w] - M);
+      den += sc * c[NCB * 16 + cb * 16 + row];
+      num += sc * *reinterpret_cast<const f32x4*>(&c[32 * NCB + (j * 64 + lane) * 4]);
+    }
+    out(cb, nd, M, den, num);
+  }
+}
+
+template <int D, int NT, int BS, int HG, int NW>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void decode_streamk_kernel(DecodeArgs a) {
+  constexpr int NC = D / 32;
+  constexpr int ND = D / 16;
+  constexpr int LS = D + 8;
+  constexpr int NTHR = 64 * NW;
+  constexpr bool UNIFORM_TILE = BS > 0 && BS % 16 == 0;
+  // Prefix items are built where a tile lies in one block and four column
+  // blocks of accumulators fit the registers.
+  constexpr bool SHARE = UNIFORM_TILE && D <= 64;
+  constexpr int NCP = kPfxColBlocks;
+  constexpr int NTP = 2;  // tiles per chunk of a prefix item (one kv head)
   constexpr int VST = NT * HG * 16 * LS;  // halves of one staging buffer (K or V) per wavefront
   constexpr int CMB = 32 * HG + HG * ND * 64 * 4;  // floats of merge state per wavefront
+  constexpr int VSTP = SHARE ? NTP * 16 * LS : 0;
+  constexpr int CMBP = SHARE ? 32 * NCP + NCP * ND * 64 * 4 : 0;
   // Per wavefront: a K and a V staging buffer; the merge state reuses the same
   // bytes at segment ends.
-  constexpr int WAVE_BYTES = (2 * VST * 2 > CMB * 4 ? 2 * VST * 2 : CMB * 4);
+  constexpr int WAVE_BYTES_0 = 2 * VST * 2 > CMB * 4 ? 2 * VST * 2 : CMB * 4;
+  constexpr int WAVE_BYTES_1 = 2 * VSTP * 2 > CMBP * 4 ? 2 * VSTP * 2 : CMBP * 4;
+  constexpr int WAVE_BYTES = WAVE_BYTES_0 > WAVE_BYTES_1 ? WAVE_BYTES_0 : WAVE_BYTES_1;
   constexpr int PER = kSkMaxSeqs / NTHR;  // sequences planned per thread
   constexpr int REC = record_floats(D);
   static_assert(PER * NTHR == kSkMaxSeqs, "plan layout");
   __shared__ __attribute__((aligned(16))) char smem[NW * WAVE_BYTES];
-  __shared__ int s_pref[kSkMaxSeqs + 1];  // sequence -> first tile position (per kv-head group)
+  // Sequence -> first list position of its items (prefix items, then pairs).
+  __shared__ int s_pos[kSkMaxSeqs + 1];
+  // Sequence -> its group's shared tiles (bits 0-7, zero: none), its member
+  // index (8-11) and the group's size (12-15).
+  __shared__ int s_info[SHARE ? kSkMaxSeqs : 1];
   __shared__ int s_wtot[NW];
   __shared__ int s_nmerge;                // pairs listed for merging
   __shared__ int s_mlist[NTHR];           // pairs whose records this workgroup completed
@@ -108,33 +488,174 @@ void decode_streamk_kernel(DecodeArgs a) {
   const int row = lane & 15;
   const int grp = lane >> 4;
   const int B = a.num_seqs;
-  const int NHG = a.hkv / HG;
+  const int Hkv = a.hkv;
+  const int NHG = Hkv / HG;
   const int bs = BS > 0 ? BS : a.bs;
   const int G = gridDim.x;
+  const bool share = SHARE && a.share;
+  // List positions of a prefix item's tiles: one per tile. A prefix tile holds
+  // one kv head (a pair's tile HG of them), but a prefix wavefront keeps a
+  // chunk of NTP one-head tiles in flight where a pair's keeps NT tiles of HG
+  // heads, and its four column blocks cost more math per byte: in a
+  // bandwidth-saturated launch its bytes take about twice as long each.
+  auto pfx_pos = [&](int pt) { return pt; };
 
-  // ---- plan: clamped lengths and the exclusive prefix of tiles per sequence ----
+  // ---- plan: lengths, sharing groups, the exclusive prefix of list positions ----
+  // Every load of the plan is issued before any is used, so that the plan
+  // costs one memory round trip: the table rows the sharing groups are found
+  // from (below), then the lengths (unconditional, indices clamped; a branch
+  // per load would wait for each in turn).
+  int rows[32];
+  const int capc = min(kPfxCapBlocks, a.max_blocks);
+  const int col = min(lane, capc - 1);
+  auto load_rows = [&](int b0) {
+#pragma unroll
+    for (int r = 0; r < 32; ++r) {
+      const int rb = min(b0 + r, B - 1);
+      rows[r] = a.bt[(int64_t)rb * a.bt_sb + (int64_t)col * a.bt_sk];
+    }
+  };
+  // The sharing compare also needs lane r's length of sequence b0 + r.
+  int wlen = 0;
+  auto load_wlen = [&](int b0) {
+    wlen = a.lens ? a.lens[min(b0 + lane, B - 1)] : a.uniform_len;
+  };
+  if (share && wave * 32 < B) {
+    load_rows(wave * 32);
+    load_wlen(wave * 32);
+  }
+  int Ls[PER];
+  if (a.lens) {
+#pragma unroll
+    for (int i = 0; i < PER; ++i) Ls[i] = a.lens[min(tid * PER + i, B - 1)];
+  } else {
+#pragma unroll
+    for (int i = 0; i < PER; ++i) Ls[i] = a.uniform_len;
+  }
+  {
+    const int cap = a.max_blocks * a.bs;
+#pragma unroll
+    for (int i = 0; i < PER; ++i)
+      Ls[i] = tid * PER + i < B ? min(max(Ls[i], 0), cap) : 0;  // as clamped_len
+  }
+  if constexpr (SHARE) {
+    if (share) {
+      // Sharing groups, found by each wavefront for its slices of 32
+      // sequences (w * 32 + 256 k ..), with no barrier: lane j holds table
+      // entry j of rows b0 .. b0 + 31 and lane r the length of sequence b0 + r;
+      // the wavefront finds, per sequence, the leading entries it shares with
+      // its predecessor, cuts runs of sharing sequences into groups of at most
+      // max_members (a group never crosses a slice) and writes each sequence's
+      // group information to s_info.
+      for (int b0 = wave * 32; b0 < B; b0 += NW * 32) {
+        if (b0 != wave * 32) {
+          load_rows(b0);
+          load_wlen(b0);
+        }
+        // Lane r: the table entries sequence b0 + r and its predecessor both
+        // hold as full blocks (at most capc).
+        const int fl = min(max(wlen, 0), a.max_blocks * a.bs) / bs;
+        const int limv = min(capc, min(fl, __shfl_up(fl, 1)));
+        // ct: lane i < 32 gets the tiles sequence b0 + i shares with b0 + i - 1
+        // (zero for the slice's first sequence: groups start at slice starts).
+        // Per sequence one compare into a 64-bit lane mask; the first mismatch
+        // or limit is found in scalar registers and written into lane r.
+        int ct = 0;
+#pragma unroll
+        for (int r = 1; r < 32; ++r) {
+          const int lim = __builtin_amdgcn_readlane(limv, r);
+          const uint64_t diff = __ballot(rows[r] != rows[r - 1]) | (lim >= 64 ? 0ull : ~0ull << lim);
+          const int c = diff ? (int)__builtin_ctzll(diff) : 64;
+          const int v = min(c * (bs / 16), 255);
+          asm volatile("v_writelane_b32 %0, %1, %2" : "+v"(ct) : "s"(v), "i"(r));
+        }
+        const int bl = b0 + lane;  // lane i < 32: sequence b0 + i
+        const bool valid = lane < 32 && bl < B;
+        if (!valid) ct = 0;
+        // Run starts (a sequence sharing nothing with its predecessor; lanes
+        // 32 .. 63 count as starts): the last at or before this lane, and the
+        // first after it, from one lane mask.
+        const uint64_t starts = __ballot(ct == 0);
+        const uint64_t upto = starts & (lane == 63 ? ~0ull : (2ull << lane) - 1);
+        const int rs = 63 - (int)__builtin_clzll(upto);  // lane 0 is a start: upto != 0
+        const uint64_t after = starts & ~(lane == 63 ? ~0ull : (2ull << lane) - 1);
+        const int nxt = after ? (int)__builtin_ctzll(after) : 64;
+        const int m = (lane - rs) % a.max_members;
+        const int gs = min(a.max_members, nxt - lane);  // meaningful at leaders (m == 0)
+        int pt = 255;
+#pragma unroll
+        for (int k = 1; k < kPfxMaxMembers; ++k) {
+          const int v = __shfl_down(ct, k);
+          if (k < gs) pt = min(pt, v);
+        }
+        // Shared when the reads it saves outweigh the prefix items' overhead.
+        const bool worth = gs > 1 && (int64_t)(gs - 1) * NHG * pt > (int64_t)Hkv * a.seg_cost;
+        const int lead = lane - m;
+        const int gsl = __shfl(gs, lead);
+        const int ptl = __shfl(worth ? pt : 0, lead);
+        if (valid) s_info[bl] = ptl ? (ptl | (m << 8) | (gsl << 12)) : 0;
+      }
+      __syncthreads();
+    }
+  }
   {
     int cnt[PER];
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
       const int b = tid * PER + i;
-      const int n = b < B ? (clamped_len(a, b) + 15) >> 4 : 0;
-      cnt[i] = n > 0 ? n + a.seg_cost : 0;  // pair width: its tiles plus the segment overhead
+      const int n = (Ls[i] + 15) >> 4;
+      int pt = 0, m = 0;
+      if constexpr (SHARE) {
+        if (share && b < B) {
+          pt = s_info[b] & 255;
+          m = (s_info[b] >> 8) & 15;
+        }
+      }
+      // Each pair: its tiles after the shared prefix plus the segment overhead;
+      // a group leader also holds the group's prefix items, one per kv head.
+      const int w = n - pt > 0 ? n - pt + a.seg_cost : 0;
+      cnt[i] = b < B ? NHG * w + (pt > 0 && m == 0 ? Hkv * (pfx_pos(pt) + a.seg_cost) : 0) : 0;
     }
     const int total = block_excl_sum<PER, NW>(cnt, s_wtot, lane, wave);
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
       const int b = tid * PER + i;
-      if (b < B) s_pref[b] = cnt[i];
+      if (b < B) s_pos[b] = cnt[i];
     }
-    if (tid == 0) s_pref[B] = total;
+    if (tid == 0) s_pos[B] = total;
     __syncthreads();
   }
+
+  // Plan lookups for sequence b: shared tiles of its group, member index,
+  // group size, and the widths of its prefix region (leaders) and pairs.
+  struct Geo {
+    int base, pw, ws, pt, m, gs;
+  };
+  auto geo_of = [&](int base, int next, int info) {
+    Geo g;
+    g.base = base;
+    g.pt = info & 255;
+    g.m = (info >> 8) & 15;
+    g.gs = info >> 12;
+    g.pw = (g.pt > 0 && g.m == 0) ? Hkv * (pfx_pos(g.pt) + a.seg_cost) : 0;
+    g.ws = (next - g.base - g.pw) / NHG;
+    return g;
+  };
+  // For a wavefront-uniform b (the segment walk): readfirstlane keeps the
+  // values in scalar registers, off the vector registers the streaming loop
+  // needs.
+  auto geo = [&](int b) {
+    return geo_of(uni(s_pos[b]), uni(s_pos[b + 1]), share ? uni(s_info[SHARE ? b : 0]) : 0);
+  };
+  // For a b that differs between the lanes (the merge of completed pairs).
+  auto geo_v = [&](int b) {
+    return geo_of(s_pos[b], s_pos[b + 1], share ? s_info[SHARE ? b : 0] : 0);
+  };
 
   // Zero-length sequences have no tiles; their rows are written as zeros.
   const int Hq = a.hkv * a.g;
   for (int b = blockIdx.x; b < B; b += G) {
-    if (s_pref[b + 1] == s_pref[b]) {
+    if (s_pos[b + 1] == s_pos[b] && geo(b).pt == 0) {
       for (int i = tid; i < Hq * D; i += NTHR) {
         const int hq = i / D;
         a.out[(int64_t)b * a.o_sb + (int64_t)hq * a.o_sh + (i - hq * D)] = (f16)0.f;
@@ -144,15 +665,14 @@ void decode_streamk_kernel(DecodeArgs a) {
 
   // Ranges: at least min_range tile positions each, at most one per
   // workgroup; workgroups beyond them get no range.
-  const int64_t T = (int64_t)NHG * s_pref[B];
-  const int64_t Gw = (T + a.min_range - 1) / a.min_range;
+  const int T = uni(s_pos[B]);
+  const int Gw = (T + a.min_range - 1) / a.min_range;
   const int Ge = (int)(Gw < G ? Gw : G);  // 0 when every sequence is empty
 
   // The first A workgroups take part. Workgroup i is dispatched to XCD i % 8;
   // renumber the A of them so that each XCD owns a contiguous run of ranges
-  // (or pairs): neighbouring sequences, which is where shared prefix blocks
-  // sit, then run on the same XCD and share its L2, and every XCD gets work
-  // when A < G.
+  // (or pairs): neighbouring sequences then run on the same XCD and share its
+  // L2, and every XCD gets work when A < G.
   const int A = a.pair_per_wg ? (B * NHG < G ? B * NHG : G) : Ge;
   if ((int)blockIdx.x >= A) return;
   const int wg = [&] {
@@ -160,55 +680,78 @@ void decode_streamk_kernel(DecodeArgs a) {
     const int xcd = blockIdx.x % kXcds, k = blockIdx.x / kXcds;
     return xcd * n8 + (xcd < rem ? xcd : rem) + k;
   }();
-  int64_t x0, x1;
+  int x0, x1;
   if (a.pair_per_wg) {
-    // Small batches of short pairs: workgroup w takes pair w whole, so no pair
-    // is cut, no partial record is written and no merge is needed.
+    // Small batches of short pairs (no sharing): workgroup w takes pair w
+    // whole, so no pair is cut, no partial record is written and no merge is
+    // needed.
     const int pb = wg / NHG;
-    const int width = s_pref[pb + 1] - s_pref[pb];
+    const int width = (uni(s_pos[pb + 1]) - uni(s_pos[pb])) / NHG;
     if (width == 0) return;  // a zero-length sequence: its rows were written above
-    x0 = (int64_t)NHG * s_pref[pb] + (int64_t)(wg - pb * NHG) * width;
+    x0 = uni(s_pos[pb]) + (wg - pb * NHG) * width;
     x1 = x0 + width;
   } else {
-    x0 = range_start(wg, T, Ge);
-    x1 = range_start(wg + 1, T, Ge);
+    x0 = (int)range_start(wg, T, Ge);
+    x1 = (int)range_start(wg + 1, T, Ge);  // once per workgroup: 64-bit is fine
   }
 
-  // First pair: the last sequence whose pairs start at or before x0.
+  // First item: in the last sequence whose items start at or before x0.
   int b;
   {
     int lo = 0, hi = B - 1;
     while (lo < hi) {
       const int mid = (lo + hi + 1) >> 1;
-      if ((int64_t)NHG * s_pref[mid] <= x0) lo = mid; else hi = mid - 1;
+      if (s_pos[mid] <= x0) lo = mid; else hi = mid - 1;
     }
-    b = lo;
+    b = uni(lo);
   }
 
-  // Byte offset of this lane's 16-byte piece within a tile, relative to the
-  // tile's first row at the group's first kv head (same for every tile).
-  uint32_t k_lane = 0, v_lane = 0;
-  if constexpr (UNIFORM_TILE) {
-    const int lrow = lane / CPR, lcol = (lane % CPR) * 8;
-    const int lhg = lcol / D, ld0 = lcol - lhg * D;
-    k_lane = (uint32_t)(2 * (lrow * a.k_st + lhg * a.k_sh + ld0));
-    v_lane = (uint32_t)(2 * (lrow * a.v_st + lhg * a.v_sh + ld0));
-  }
   char* my_smem = smem + wave * WAVE_BYTES;
   f16* kst = reinterpret_cast<f16*>(my_smem);  // K staging
-  f16* vst = kst + VST;                          // V staging
-
-  // Partial records, two per range: slot 2 w + 1 for the pair range w cuts at
-  // its end, slot 2 w for the pair it continues from earlier ranges.
+  // Partial records (float offsets from a.recs): two slots per workgroup
+  // (slot 2 w + 1 for the item range w cuts at its end, slot 2 w for the item
+  // it continues from earlier ranges), each of slot_recs records (one per kv
+  // head of a pair, or per column block of a prefix item); then, for items a
+  // range holds whole, per (sequence, kv head): a suffix record of a sharing
+  // member's pair (Q) and a prefix record (P: column block cb of the group led
+  // by sequence b is sequence b + cb's entry).
+  const int SLOT = a.slot_recs * REC;
+  const int64_t QBASE = (int64_t)2 * G * SLOT;
+  const int64_t PBASE = QBASE + (int64_t)B * Hkv * REC;
+  auto slot_base = [&](int w, bool first) { return (int64_t)(2 * w + (first ? 1 : 0)) * SLOT; };
   const auto rec_rsrc = tile_rsrc(a.recs, a.recs_bytes);
 
-  // The ranges wa .. wa + nrec - 1 a cut pair spans.
-  auto pair_span = [&](int p, int& wa, int& nrec) {
+  // The ranges wa .. wa + cnt - 1 that an item's tile positions ps .. ps + n - 1
+  // span. In 32-bit arithmetic when T * Ge fits (any realistic launch: 64-bit
+  // division is a long instruction sequence, and the merge computes this per
+  // record list).
+  const bool small_list = (int64_t)T * Ge < ((int64_t)1 << 31);
+  auto wg_at = [&](int x) {
+    return small_list ? (int)((unsigned)((x + 1) * Ge - 1) / (unsigned)T) : wg_of(x, T, Ge);
+  };
+  auto span = [&](int ps, int n, int& wa, int& cnt) {
+    if (n <= 0) {
+      wa = 0;
+      cnt = 0;
+      return;
+    }
+    wa = wg_at(ps);
+    cnt = wg_at(ps + n - 1) - wa + 1;
+  };
+  // Records that make up pair p's head hh: its suffix records (ns of them from
+  // ranges wa_s ..) then its prefix records (np from ranges wa_p ..).
+  auto contributions = [&](int p, int hh, Geo& g, int& wa_s, int& ns, int& wa_p, int& np) {
     const int pb = p / NHG;
-    const int nt = s_pref[pb + 1] - s_pref[pb] - a.seg_cost;
-    const int64_t ps = (int64_t)NHG * s_pref[pb] + (int64_t)(p - pb * NHG) * (nt + a.seg_cost) + a.seg_cost;
-    wa = wg_of(ps, T, Ge);
-    nrec = wg_of(ps + nt - 1, T, Ge) - wa + 1;
+    const int hg0 = p - pb * NHG;
+    g = geo_v(pb);
+    span(g.base + g.pw + hg0 * g.ws + a.seg_cost, g.ws - a.seg_cost, wa_s, ns);
+    np = 0;
+    wa_p = 0;
+    if (g.pt > 0) {
+      const int wp = pfx_pos(g.pt) + a.seg_cost;
+      const int h = hg0 * HG + hh;
+      span(s_pos[pb - g.m] + h * wp + a.seg_cost, pfx_pos(g.pt), wa_p, np);
+    }
   };
 
   // Arrivals this workgroup has counted and not yet resolved: thread t < npend
@@ -218,24 +761,35 @@ void decode_streamk_kernel(DecodeArgs a) {
   int my_old = 0;
 
   // Resolves the counted arrivals: a pair whose count this workgroup completed
-  // is merged here -- its records in range order, by an online log-sum-exp over
-  // 16-byte device-coherent loads (each thread four accumulators of one query
-  // head, eight records in flight), all such pairs of the workgroup at once --
-  // and its counter is reset to zero for the next launch.
+  // is merged here -- its records in a fixed order (suffix ranges, then prefix
+  // ranges), by an online log-sum-exp over 16-byte device-coherent loads (each
+  // thread four accumulators of one query head, eight records in flight), all
+  // such pairs of the workgroup at once -- and its counter is reset to zero
+  // for the next launch.
   auto resolve = [&]() {
+    const int tid = wave * 64 + fresh_lane();
     const int my_pair = tid < npend ? s_mlist[tid] : 0;
     if (tid == 0) s_nmerge = 0;
     __syncthreads();
     if (tid < npend) {
-      int wa, nrec;
-      pair_span(my_pair, wa, nrec);
-      if (my_old == nrec - 1) s_mlist[atomicAdd(&s_nmerge, 1)] = my_pair;
+      int expect = 0;
+#pragma unroll
+      for (int hh = 0; hh < HG; ++hh) {
+        Geo g;
+        int wa_s, ns, wa_p, np;
+        contributions(my_pair, hh, g, wa_s, ns, wa_p, np);
+        expect += (hh == 0 ? ns : 0) + np;
+      }
+      if (my_old == expect - 1) s_mlist[atomicAdd(&s_nmerge, 1)] = my_pair;
     }
     __syncthreads();
     const int nmg = s_nmerge;
     constexpr int DQ = D / 4;
     const int per = HG * a.g * DQ;
+    const int mpb = 16 / a.g;
     for (int it = tid; it < nmg * per; it += NTHR) {
+      // Item: four accumulators (dq) of query head qr of kv head h of one
+      // merged pair.
       const int e = it / per;
       int rem = it - e * per;
       const int hh = rem / (a.g * DQ);
@@ -243,8 +797,26 @@ void decode_streamk_kernel(DecodeArgs a) {
       const int qr = rem / DQ;
       const int dq = rem - qr * DQ;
       const int p = s_mlist[e];
-      int wa, n;
-      pair_span(p, wa, n);
+      const int pb = p / NHG;
+      const int h = (p - pb * NHG) * HG + hh;
+      Geo g;
+      int wa_s, ns, wa_p, np;
+      contributions(p, hh, g, wa_s, ns, wa_p, np);
+      const int n = ns + np;
+      // Record k: a whole suffix or prefix item of a sharing member has its
+      // own record; cut items use range slots. A prefix item's record is one
+      // of its column blocks, whose 16 rows hold members cb * mpb .. cb * mpb +
+      // mpb - 1 times the query group: this member's rows start at rsh.
+      const int cbm = g.m / mpb;
+      const int rsh = (g.m - cbm * mpb) * a.g;
+      auto rec_of = [&](int k) -> int {
+        if (k < ns)
+          return (int)(ns == 1 ? QBASE + ((int64_t)pb * Hkv + h) * REC
+                               : slot_base(wa_s + k, k == 0) + (int64_t)hh * REC);
+        const int j = k - ns;
+        return (int)(np == 1 ? PBASE + ((int64_t)(pb - g.m + cbm) * Hkv + h) * REC
+                             : slot_base(wa_p + j, j == 0) + (int64_t)cbm * REC);
+      };
       float M = kNegInf, den = 0.f;
       f32x4 num = {0.f, 0.f, 0.f, 0.f};
       for (int k0 = 0; k0 < n; k0 += 8) {
@@ -252,13 +824,17 @@ void decode_streamk_kernel(DecodeArgs a) {
         f32x4 av[8];
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
-          const int kk = k0 + k < n ? k0 + k : 0;
-          const int slot = 2 * (wa + kk) + (kk == 0 ? 1 : 0);
-          const int base = (slot * HG + hh) * REC;
-          mv[k] = load_coherent4(rec_rsrc, 4 * (base + qr));
-          lv[k] = load_coherent4(rec_rsrc, 4 * (base + 16 + qr));
-          av[k] = load_coherent16(rec_rsrc, 4 * (base + 32 + qr * D + dq * 4));
-          if (k0 + k >= n) mv[k] = kNegInf;
+          // Padding past the item's records reads at an offset past the record
+          // area: the buffer returns zeros and touches no memory.
+          const bool live = k0 + k < n;
+          const int kk = live ? k0 + k : 0;
+          const int base = rec_of(kk);
+          const int r = (kk < ns ? 0 : rsh) + qr;  // this query head's row of the record
+          constexpr int kOut = 0x7ffffff0;
+          mv[k] = load_coherent4(rec_rsrc, live ? 4 * (base + r) : kOut);
+          lv[k] = load_coherent4(rec_rsrc, live ? 4 * (base + 16 + r) : kOut);
+          av[k] = load_coherent16(rec_rsrc, live ? 4 * (base + 32 + r * D + dq * 4) : kOut);
+          if (!live) mv[k] = kNegInf;
         }
         float mb = M;
 #pragma unroll
@@ -278,9 +854,8 @@ void decode_streamk_kernel(DecodeArgs a) {
       f16x4 ov;
 #pragma unroll
       for (int c = 0; c < 4; ++c) ov[c] = (f16)(num[c] * inv);
-      const int pb = p / NHG, hgp = p - pb * NHG;
       *reinterpret_cast<f16x4*>(a.out + (int64_t)pb * a.o_sb +
-                                (int64_t)((hgp * HG + hh) * a.g + qr) * a.o_sh + dq * 4) = ov;
+                                (int64_t)(h * a.g + qr) * a.o_sh + dq * 4) = ov;
     }
     for (int e = tid; e < nmg; e += NTHR)
       __hip_atomic_store(a.cnt + s_mlist[e], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -288,51 +863,97 @@ void decode_streamk_kernel(DecodeArgs a) {
     npend = 0;
   };
 
+  // Publishes a segment's records: every thread waits for its coherent stores
+  // to complete, then one arrival is counted for each of the n pairs pair_of(i)
+  // the records belong to. The returned counts are only needed when the
+  // workgroup resolves its arrivals, so the atomics' latency overlaps the rest
+  // of the range.
+  auto arrive = [&](int n, auto pair_of) {
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (tid >= npend && tid < npend + n) {
+      const int p = pair_of(tid - npend);
+      s_mlist[tid] = p;
+      my_old = __hip_atomic_fetch_add(a.cnt + p, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    npend += n;
+  };
 
-  // Segment order: a range starts with at most one segment that continues a
-  // pair begun in an earlier range. It is processed last, so every workgroup
-  // starts on the first tiles of a pair: the leading blocks of all sequences
-  // -- where sequences share prefix blocks -- are read close together in time
-  // and repeated reads of a shared block find it in the L2 / MALL.
-  int64_t cont_end = x0;  // end of the leading continuation segment (x0 if none)
+  // Item containing list position x (in sequence b's items): kind (0 pair,
+  // 1 prefix item), index (kv-head group, or kv head), and its positions.
+  auto locate = [&](int bb, int x, int& kind, int& idx, int& is, int& ie, Geo& g) {
+    g = geo(bb);
+    const int o = x - g.base;
+    if (o < g.pw) {
+      const int wp = g.pw / Hkv;
+      kind = 1;
+      idx = o / wp;
+      is = g.base + idx * wp;
+      ie = is + wp;
+    } else {
+      kind = 0;
+      idx = (o - g.pw) / g.ws;
+      is = g.base + g.pw + idx * g.ws;
+      ie = is + g.ws;
+    }
+  };
+
+  // Segment order. The range's prefix-item segments go first (step 0), so
+  // that the prefix records are complete early and the members' own segments
+  // -- spread over many workgroups -- complete their counts and merge; a prefix
+  // item finished last would leave one workgroup merging its whole group at
+  // the end of the launch. Then the pairs (steps 1 and 2): a range starts with
+  // at most one segment that continues an item begun in an earlier range; it
+  // is processed last, so every workgroup starts on the first tiles of a pair:
+  // the leading blocks of all sequences -- where sequences share prefix blocks
+  // that no prefix item covers -- are read close together in time and repeated
+  // reads find them in the L2 / MALL.
+  const int b_first = b;
+  int cont_end = x0;  // end of the leading continuation segment (x0 if none)
   {
-    const int64_t base0 = (int64_t)NHG * s_pref[b];
-    const int nt0 = s_pref[b + 1] - s_pref[b];
-    const int64_t ps0 = base0 + (x0 - base0) / nt0 * nt0;
-    if (ps0 < x0) cont_end = ps0 + nt0 < x1 ? ps0 + nt0 : x1;
+    int kind, idx;
+    int is, ie;
+    Geo g;
+    locate(b, x0, kind, idx, is, ie, g);
+    if (is < x0) cont_end = ie < x1 ? ie : x1;
   }
   const int b_cont = b;
-  if (cont_end > x0 && cont_end < x1 && cont_end >= (int64_t)NHG * s_pref[b + 1]) {
+  if (cont_end > x0 && cont_end < x1 && cont_end >= uni(s_pos[b + 1])) {
     ++b;
-    while (b < B - 1 && s_pref[b + 1] == s_pref[b]) ++b;
+    while (b < B - 1 && uni(s_pos[b + 1]) == uni(s_pos[b])) ++b;
   }
 
-  for (int pass = 0; pass < 2; ++pass) {
-  int64_t x = pass == 0 ? cont_end : x0;
-  const int64_t x_end = pass == 0 ? x1 : cont_end;
-  if (pass == 1) b = b_cont;
+  const int b_pairs = b;
+  for (int step = share ? 0 : 1; step < 3; ++step) {
+  const int want_kind = step == 0 ? 1 : 0;
+  int x = step == 0 ? x0 : (step == 1 ? cont_end : x0);
+  const int x_end = step == 0 ? x1 : (step == 1 ? x1 : cont_end);
+  b = step == 0 ? b_first : (step == 1 ? b_pairs : b_cont);
   while (x < x_end) {
-    const int nt_b = s_pref[b + 1] - s_pref[b];  // pair width, seg_cost included
-    const int64_t base = (int64_t)NHG * s_pref[b];
-    const int hg0 = (int)((x - base) / nt_b);
-    const int64_t pstart = base + (int64_t)hg0 * nt_b;
-    const int64_t pend = pstart + nt_b;
-    // Segment bounds in real tiles (the pair's first seg_cost positions stand
-    // for its fixed overhead and hold no tiles), wavefront-uniform by
-    // construction; readfirstlane makes that visible to the compiler, so the
-    // loop below keeps uniform branches (a branch it must treat as divergent
-    // gets restructured into paths that skip loads, which spoils the wait
-    // counts of the load pipeline).
-    const int s0 = __builtin_amdgcn_readfirstlane(max((int)(x - pstart) - a.seg_cost, 0));
-    const int s1 = __builtin_amdgcn_readfirstlane(
-        max((int)((x1 < pend ? x1 : pend) - pstart) - a.seg_cost, 0));
-    const bool first = s0 == 0;
+    // Room for this segment's arrivals in the pending list.
+    if (npend > NTHR - kPfxMaxMembers - HG) resolve();
+    int kind, idx;
+    int pstart, pend;
+    Geo g;
+    locate(b, x, kind, idx, pstart, pend, g);
+    // Segment bounds in the item's tile positions (its first seg_cost
+    // positions stand for its fixed overhead and hold no tiles),
+    // wavefront-uniform by construction; readfirstlane makes that visible to
+    // the compiler, so the loops keep uniform branches (a branch it must treat
+    // as divergent gets restructured into paths that skip loads, which spoils
+    // the wait counts of the load pipeline).
+    const int r0 = uni(max(x - pstart - a.seg_cost, 0));
+    const int r1 = uni(max((x1 < pend ? x1 : pend) - pstart - a.seg_cost, 0));
+    const bool first = r0 == 0;
     const bool last = pend <= x1;
-    if (s1 > s0) {  // else the range holds only overhead positions of this pair
+    if (r1 > r0 && kind == 0 && want_kind == 0) {
+      // ---- a pair: kv heads h0 .. h0 + HG - 1 of sequence b, tiles after its prefix ----
+      const int lane = fresh_lane();
+      const int row = lane & 15, grp = lane >> 4;
       const int L = __builtin_amdgcn_readfirstlane(clamped_len(a, b));
-      const int h0 = hg0 * HG;  // first kv head of the group
-
-      // ---- this wavefront's share of the segment ----
+      const int h0 = idx * HG;
+      const int s0 = g.pt + r0, s1 = g.pt + r1;
+      const bool whole = first && last;
       f16x8 qf[HG][NC];
       {
         const int gq = min(row, a.g - 1);
@@ -346,97 +967,6 @@ void decode_streamk_kernel(DecodeArgs a) {
           }
         }
       }
-      const int32_t* btrow = a.bt + (int64_t)b * a.bt_sb;
-      const int tok_fallback = s0 * 16;  // a valid token of this segment
-
-      // Natural-layout loads: instruction i of a tile gives lane l the 16-byte
-      // chunk f = 64 i + l of the tile's 16 rows x (HG * D) halves, i.e. row
-      // f / CPR, halves (f % CPR) * 8 of the row's head-group slice. Each
-      // instruction thus reads whole row slices (whole cache lines).
-      auto nat_row = [&](int i) { return (64 * i + lane) / CPR; };
-      auto nat_col = [&](int i) { return ((64 * i + lane) % CPR) * 8; };
-      auto row_token = [&](int ti, int r) {
-        const int t = ti * 16 + r;
-        return (ti < s1 && t < L) ? t : tok_fallback;
-      };
-      auto load_ids = [&](int k, int (&ids)[NT][NID]) {
-#pragma unroll
-        for (int nt = 0; nt < NT; ++nt)
-#pragma unroll
-          for (int j = 0; j < NID; ++j) {
-            // A uniform tile lies in one block; otherwise each lane looks up the
-            // block of its own row (also when one instruction covers the tile).
-            const int t = row_token(s0 + k * NT + nt, UNIFORM_TILE ? 0 : nat_row(j));
-            if constexpr (UNIFORM_TILE)
-              ids[nt][j] = load_uniform(btrow + (int64_t)blk_of<BS>(t, bs) * a.bt_sk);
-            else
-              ids[nt][j] = btrow[(int64_t)blk_of<BS>(t, bs) * a.bt_sk];
-          }
-      };
-      auto load_kv = [&](int k, const int (&ids)[NT][NID], u32x4 (&kb)[NT][NI], u32x4 (&vb)[NT][NI]) {
-#pragma unroll
-        for (int nt = 0; nt < NT; ++nt) {
-          const int ti = s0 + k * NT + nt;
-          if constexpr (UNIFORM_TILE) {
-            // Unconditional: a tile past the segment gets an empty resource.
-            const int64_t id = min(max(ids[nt][0], 0), a.num_blocks - 1);
-            const int64_t r0 = (ti * 16) % BS;
-            const int nb = ti < s1 ? 0x7fffffff : 0;
-            const auto kr = tile_rsrc(a.k + id * a.k_sb + r0 * a.k_st + (int64_t)h0 * a.k_sh, nb);
-            const auto vr = tile_rsrc(a.v + id * a.v_sb + r0 * a.v_st + (int64_t)h0 * a.v_sh, nb);
-#pragma unroll
-            for (int i = 0; i < NI; ++i) {
-              kb[nt][i] = load_tile(kr, k_lane, (int)(2 * i * RS * a.k_st));
-              vb[nt][i] = load_tile(vr, v_lane, (int)(2 * i * RS * a.v_st));
-            }
-          } else if (ti < s1) {
-#pragma unroll
-            for (int i = 0; i < NI; ++i) {
-              const int t = row_token(ti, nat_row(i));
-              const int64_t id = min(max(ids[nt][i], 0), a.num_blocks - 1);
-              const int64_t off = off_of<BS>(t, bs);
-              const int col = nat_col(i);
-              const int hg = col / D;
-              const int d0 = col - hg * D;
-              kb[nt][i] = load_stream(a.k + id * a.k_sb + off * a.k_st + (int64_t)(h0 + hg) * a.k_sh + d0);
-              vb[nt][i] = load_stream(a.v + id * a.v_sb + off * a.v_st + (int64_t)(h0 + hg) * a.v_sh + d0);
-            }
-          }
-        }
-      };
-      // Writes one tile's rows (natural layout) into the staging buffer laid out
-      // [tile][head][row][LS]; rows past the sequence end are zeroed when asked.
-      auto stage = [&](int k, u32x4 (&buf)[NT][NI], f16* dst, bool zero_tail) {
-#pragma unroll
-        for (int nt = 0; nt < NT; ++nt) {
-          const int ti = s0 + k * NT + nt;
-          if (ti < s1) {
-#pragma unroll
-            for (int i = 0; i < NI; ++i) {
-              const int r = nat_row(i);
-              const int col = nat_col(i);
-              const int hg = col / D;
-              const int d0 = col - hg * D;
-              *reinterpret_cast<u32x4*>(&dst[((nt * HG + hg) * 16 + r) * LS + d0]) = buf[nt][i];
-            }
-            // Rows past the sequence end are overwritten with zeros in LDS (not
-            // selected in registers: a select on freshly loaded registers makes
-            // the compiler wait for those loads where it places the select).
-            if (zero_tail && ti * 16 + 16 > L) {  // wavefront-uniform: the last tile only
-#pragma unroll
-              for (int i = 0; i < NI; ++i) {
-                const int r = nat_row(i);
-                const int col = nat_col(i);
-                const int hg = col / D;
-                const int d0 = col - hg * D;
-                if (ti * 16 + r >= L)
-                  *reinterpret_cast<f16x8*>(&dst[((nt * HG + hg) * 16 + r) * LS + d0]) = zero8();
-              }
-            }
-          }
-        }
-      };
-
       float m_run[HG], l_run[HG];
       f32x4 acc[HG][ND];
 #pragma unroll
@@ -446,185 +976,13 @@ void decode_streamk_kernel(DecodeArgs a) {
 #pragma unroll
         for (int i = 0; i < ND; ++i) acc[hg][i] = f32x4{0.f, 0.f, 0.f, 0.f};
       }
-
-      // Both K and V of chunk k go to LDS first, which frees their registers for
-      // the loads of the chunk two steps ahead; the math then reads LDS only.
-      auto stage_both = [&](int k, u32x4 (&kb)[NT][NI], u32x4 (&vb)[NT][NI]) {
-        stage(k, kb, kst, false);
-        stage(k, vb, vst, true);  // V rows past the sequence end as zeros: 0 * garbage is never NaN
-        wave_lds_fence();
-      };
-      auto compute = [&](int k) {
-        float xs[NT][HG][4];
-        float mloc[HG];
-#pragma unroll
-        for (int hg = 0; hg < HG; ++hg) mloc[hg] = kNegInf;
-#pragma unroll
-        for (int nt = 0; nt < NT; ++nt) {
-          const int ti = s0 + k * NT + nt;
-#pragma unroll
-          for (int hg = 0; hg < HG; ++hg) {
-            if (ti < s1) {
-              const f16* kt = kst + ((nt * HG + hg) * 16 + row) * LS + grp * 8;
-              f32x4 s = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-              for (int c = 0; c < NC; ++c)
-                s = __builtin_amdgcn_mfma_f32_16x16x32_f16(*reinterpret_cast<const f16x8*>(kt + 32 * c),
-                                                           qf[hg][c], s, 0, 0, 0);
-              if (ti * 16 + 16 <= L) {  // wavefront-uniform: only the last tile is partial
-#pragma unroll
-                for (int r = 0; r < 4; ++r) xs[nt][hg][r] = s[r] * a.scale_log2;
-              } else {
-#pragma unroll
-                for (int r = 0; r < 4; ++r)
-                  xs[nt][hg][r] = ti * 16 + grp * 4 + r < L ? s[r] * a.scale_log2 : kNegInf;
-              }
-#pragma unroll
-              for (int r = 0; r < 4; ++r) mloc[hg] = fmaxf(mloc[hg], xs[nt][hg][r]);
-            } else {
-#pragma unroll
-              for (int r = 0; r < 4; ++r) xs[nt][hg][r] = kNegInf;
-            }
-          }
-        }
-#pragma unroll
-        for (int hg = 0; hg < HG; ++hg) {
-          float m = mloc[hg];
-          m = fmaxf(m, __shfl_xor(m, 16));
-          m = fmaxf(m, __shfl_xor(m, 32));
-          const float m_new = fmaxf(m_run[hg], m);
-          const float alpha = fast_exp2(m_run[hg] - m_new);
-          l_run[hg] *= alpha;
-#pragma unroll
-          for (int i = 0; i < ND; ++i) acc[hg][i] *= alpha;
-          m_run[hg] = m_new;
-        }
-#pragma unroll
-        for (int nt = 0; nt < NT; ++nt) {
-          const int ti = s0 + k * NT + nt;
-          if (ti < s1) {
-#pragma unroll
-            for (int hg = 0; hg < HG; ++hg) {
-              f16x4 ph, pl;
-#pragma unroll
-              for (int r = 0; r < 4; ++r) {
-                const float pr = fast_exp2(xs[nt][hg][r] - m_run[hg]);
-                l_run[hg] += pr;
-                const f16 hi = (f16)pr;
-                ph[r] = hi;
-                pl[r] = (f16)(pr - (float)hi);
-              }
-              // V^T operand: lane (row, grp) needs V[4 grp + r][16 nd + row], r = 0..3,
-              // which one transposing read of rows 4 grp..4 grp+3 delivers.
-              const f16* vt = vst + ((nt * HG + hg) * 16 + grp * 4 + (row >> 2)) * LS + (row & 3) * 4;
-#pragma unroll
-              for (int nd = 0; nd < ND; ++nd) {
-                const f16x4 av = lds_read_tr16(vt + nd * 16);
-                acc[hg][nd] = __builtin_amdgcn_mfma_f32_16x16x16f16(av, ph, acc[hg][nd], 0, 0, 0);
-                acc[hg][nd] = __builtin_amdgcn_mfma_f32_16x16x16f16(av, pl, acc[hg][nd], 0, 0, 0);
-              }
-            }
-          }
-        }
-        wave_lds_fence();
-      };
-
-      // Wavefront-local pipeline over this wavefront's chunks: wavefront w
-      // takes chunks w, w + NW, w + 2 NW, ... A fixed assignment (rather than
-      // claims from a shared counter, which let faster wavefronts take more
-      // chunks) keeps the summation order, and so the result bits, the same
-      // on every run; it costs about 1% at large batches. Step s computes chunk c_s: K/V register sets Y0/Y1 hold steps s and
-      // s+1, id sets X0/X1 the block ids of steps s+2 and s+3. At step s: stage
-      // Y[s%2] into LDS, reuse it for the loads of step s+2 (ids in X[s%2]),
-      // claim step s+3 and fetch its ids into X[(s+1)%2], then compute step s.
-      // Claims are increasing per wavefront, so the first claim past the end
-      // ends its work; loads of such chunks are issued anyway (empty resources,
-      // clamped table reads) so that no branch separates them.
-      const int nck = __builtin_amdgcn_readfirstlane((s1 - s0 + NT - 1) / NT);
-      int next_chunk = wave;
-      auto claim = [&]() {
-        const int c = next_chunk;
-        next_chunk += NW;
-        return c;
-      };
-      {
-        u32x4 kb0[NT][NI], vb0[NT][NI], kb1[NT][NI], vb1[NT][NI];
-        int ids0[NT][NID], ids1[NT][NID];
-        int c0 = claim();
-        int c1 = claim();
-        int c2 = claim();
-        load_ids(c0, ids0);
-        load_ids(c1, ids1);
-        // The scheduler must keep the loads of step 0 ahead of those of step 1:
-        // the loop's waits count on the older buffer being the one staged first.
-        load_kv(c0, ids0, kb0, vb0);
-        __builtin_amdgcn_sched_barrier(0);
-        load_kv(c1, ids1, kb1, vb1);
-        __builtin_amdgcn_sched_barrier(0);
-        load_ids(c2, ids0);
-        // Two steps per trip, one exit: both steps issue their loads on every
-        // trip and only the LDS staging and the math of a step past the end are
-        // skipped, so every path through the loop issues the same loads.
-        while (c0 < nck) {
-          stage_both(c0, kb0, vb0);
-          load_kv(c2, ids0, kb0, vb0);
-          const int c3 = claim();
-          load_ids(c3, ids1);
-          compute(c0);
-          const bool more = c1 < nck;
-          if (more) stage_both(c1, kb1, vb1);
-          load_kv(c3, ids1, kb1, vb1);
-          const int c4 = claim();
-          load_ids(c4, ids0);
-          if (more) compute(c1);
-          c0 = c2;
-          c1 = c3;
-          c2 = c4;
-        }
-      }
-
-      // ---- merge the wavefronts' states through LDS ----
-      // Every wavefront stores its maxima and denominators per head and its
-      // accumulators in register layout (chunk j = hg * ND + nd: one f32x4 per
-      // lane, so the 16-byte LDS writes are conflict-free). Wavefront w then
-      // combines chunks j = w, w + NW, ... of all wavefronts and stores them.
-      float* cm = reinterpret_cast<float*>(my_smem);
-      __syncthreads();  // every wavefront is done with its staging buffers
-#pragma unroll
-      for (int hg = 0; hg < HG; ++hg) {
-        float l = l_run[hg];
-        l += __shfl_xor(l, 16);
-        l += __shfl_xor(l, 32);
-        if (grp == 0) {
-          cm[hg * 16 + row] = m_run[hg];
-          cm[HG * 16 + hg * 16 + row] = l;
-        }
-#pragma unroll
-        for (int nd = 0; nd < ND; ++nd)
-          *reinterpret_cast<f32x4*>(&cm[32 * HG + ((hg * ND + nd) * 64 + lane) * 4]) = acc[hg][nd];
-      }
-      __syncthreads();
-      for (int j = wave; j < HG * ND; j += NW) {
-        const int hg = j / ND;
-        const int nd = j - hg * ND;
-        float mw[NW];
-        float M = kNegInf;
-#pragma unroll
-        for (int w = 0; w < NW; ++w) {
-          mw[w] = reinterpret_cast<const float*>(smem + w * WAVE_BYTES)[hg * 16 + row];
-          M = fmaxf(M, mw[w]);
-        }
-        float den = 0.f;
-        f32x4 num = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int w = 0; w < NW; ++w) {
-          const float* c = reinterpret_cast<const float*>(smem + w * WAVE_BYTES);
-          const float sc = mw[w] == kNegInf ? 0.f : fast_exp2(mw[w] - M);
-          den += sc * c[HG * 16 + hg * 16 + row];
-          num += sc * *reinterpret_cast<const f32x4*>(&c[32 * HG + (j * 64 + lane) * 4]);
-        }
+      stream_tiles<D, BS, HG, HG, NT, false, NW>(a, a.bt + (int64_t)b * a.bt_sb, h0, s0, s1, L, HG,
+                                                 qf, kst, kst + VST, wave, lane, m_run, l_run, acc);
+      const bool final_out = whole && g.pt == 0;
+      merge_waves<D, HG, NW>(smem, WAVE_BYTES, wave, lane, m_run, l_run, acc, HG,
+                             [&](int hg, int nd, float M, float den, f32x4 num) {
         if (row < a.g) {
-          if (first && last) {
+          if (final_out) {
             const float inv = den > 0.f ? 1.f / den : 0.f;
             f16x4 o;
 #pragma unroll
@@ -632,7 +990,8 @@ void decode_streamk_kernel(DecodeArgs a) {
             *reinterpret_cast<f16x4*>(a.out + (int64_t)b * a.o_sb +
                                       (int64_t)((h0 + hg) * a.g + row) * a.o_sh + nd * 16 + grp * 4) = o;
           } else {
-            const int rb = ((wg * 2 + (first ? 1 : 0)) * HG + hg) * REC;
+            const int rb = (int)(whole ? QBASE + ((int64_t)b * Hkv + h0 + hg) * REC
+                                       : slot_base(wg, first) + (int64_t)hg * REC);
             if (grp == 0 && nd == 0) {
               store_coherent(a.recs + rb + row, M);
               store_coherent(a.recs + rb + 16 + row, den);
@@ -640,36 +999,80 @@ void decode_streamk_kernel(DecodeArgs a) {
             store_coherent16(rec_rsrc, 4 * (rb + 32 + row * D + nd * 16 + grp * 4), num);
           }
         }
-      }
-      if (!(first && last)) {
-        // Publish the record: every thread waits for its coherent stores to
-        // complete, then one arrival is counted for the pair. The returned
-        // count is only needed when the workgroup resolves its arrivals, so
-        // the atomic's latency overlaps the rest of the range.
-        __builtin_amdgcn_s_waitcnt(0);
-        __syncthreads();
-        if (tid == npend) {
-          s_mlist[tid] = b * NHG + hg0;
-          my_old = __hip_atomic_fetch_add(a.cnt + b * NHG + hg0, 1, __ATOMIC_RELAXED,
-                                          __HIP_MEMORY_SCOPE_AGENT);
-        }
-        ++npend;
+      });
+      if (!final_out) {
+        const int p = b * NHG + idx;
+        arrive(1, [&](int) { return p; });
       }
       __syncthreads();  // the merge state aliases the staging buffers of the next segment
     }
+    if constexpr (SHARE) {
+      if (r1 > r0 && kind == 1 && want_kind == 1) {
+        // ---- a prefix item: kv head h, the shared tiles of the group led by b ----
+        const int lane = fresh_lane();
+        const int row = lane & 15, grp = lane >> 4;
+        const int L = __builtin_amdgcn_readfirstlane(clamped_len(a, b));
+        const int h = idx;
+        const int s0 = r0, s1 = r1;
+        const int mpb = 16 / a.g;  // members per column block
+        const int gs = g.gs;
+        const int ncb = __builtin_amdgcn_readfirstlane((gs + mpb - 1) / mpb);
+        const bool whole = first && last;
+        // Column row of block cb: query head row % g of member cb * mpb + row / g.
+        const int mrow = row / a.g, qh = row - mrow * a.g;
+        const bool col_ok = mrow < mpb;
+        f16x8 qf[NCP][NC];
+#pragma unroll
+        for (int cb = 0; cb < NCP; ++cb) {
+          const int mm = cb * mpb + mrow;
+          const bool ok = col_ok && mm < gs;
+          const f16* qp = a.q + (int64_t)(b + (ok ? mm : 0)) * a.q_sb +
+                          (int64_t)(h * a.g + qh) * a.q_sh + grp * 8;
+#pragma unroll
+          for (int c = 0; c < NC; ++c) {
+            const f16x8 t = *reinterpret_cast<const f16x8*>(qp + 32 * c);
+            qf[cb][c] = ok ? t : zero8();
+          }
+        }
+        float m_run[NCP], l_run[NCP];
+        f32x4 acc[NCP][ND];
+#pragma unroll
+        for (int cb = 0; cb < NCP; ++cb) {
+          m_run[cb] = kNegInf;
+          l_run[cb] = 0.f;
+#pragma unroll
+          for (int i = 0; i < ND; ++i) acc[cb][i] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+        stream_tiles<D, BS, 1, NCP, NTP, true, NW>(a, a.bt + (int64_t)b * a.bt_sb, h, s0, s1, L,
+                                                   ncb, qf, kst, kst + VSTP, wave, lane, m_run,
+                                                   l_run, acc);
+        merge_waves<D, NCP, NW>(smem, WAVE_BYTES, wave, lane, m_run, l_run, acc, ncb,
+                                [&](int cb, int nd, float M, float den, f32x4 num) {
+          // Column block cb is one record: row = column (member, query head).
+          if (col_ok && cb * mpb + mrow < gs) {
+            const int rb = (int)(whole ? PBASE + ((int64_t)(b + cb) * Hkv + h) * REC
+                                       : slot_base(wg, first) + (int64_t)cb * REC);
+            if (grp == 0 && nd == 0) {
+              store_coherent(a.recs + rb + row, M);
+              store_coherent(a.recs + rb + 16 + row, den);
+            }
+            store_coherent16(rec_rsrc, 4 * (rb + 32 + row * D + nd * 16 + grp * 4), num);
+          }
+        });
+        const int hq = h / HG;
+        arrive(gs, [&](int i) { return (b + i) * NHG + hq; });
+        __syncthreads();  // the merge state aliases the staging buffers of the next segment
+      }
+    }
     x = pend;
-    if (x < x_end && x >= (int64_t)NHG * s_pref[b + 1]) {
+    if (x < x_end && x >= uni(s_pos[b + 1])) {
       ++b;
-      while (b < B - 1 && s_pref[b + 1] == s_pref[b]) ++b;
+      while (b < B - 1 && uni(s_pos[b + 1]) == uni(s_pos[b])) ++b;
     }
   }
   }
 
-  // ---- pairs cut by range boundaries: the last workgroup to arrive merges ----
-  // A pair spanning ranges wa..wb has one record per range (wa's tail slot,
-  // the others' head slots); the workgroup whose arrival completes the count
-  // combines them. A range cuts at most two pairs, so at most two arrivals
-  // are pending here.
+  // ---- pairs whose arrivals this workgroup completed: merge their records ----
   resolve();
 }
 
@@ -716,6 +1119,12 @@ hipError_t launch_sk_bs(const DecodeArgs& a, hipStream_t s) {
 }
 
 }  // namespace
+
+// Whether the kernel launched for these arguments builds prefix items (the
+// host sizes the workspace and sets a.share only then).
+bool streamk_can_share(const DecodeArgs& a, int D) {
+  return D <= 64 && (a.bs == 16 || a.bs == 32) && tile_offsets_fit(a, D, a.head_group);
+}
 
 // Kv heads a wavefront handles together for this shape.
 hipError_t launch_decode_streamk(const DecodeArgs& a, int D, hipStream_t s) {
