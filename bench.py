@@ -286,16 +286,17 @@ def prefill_benchmark(dev, seed, B=8, cached=2048, new=512, iters=30, warmup=5):
 
 
 def attention_share_ms(dev, runner, seqs, iters=20):
-    """The decode step's paged-attention work timed on its own: per layer one fused RoPE +
-    K/V write and one batched attention call at the batch's final lengths, times the layers.
+    """The decode step's paged-attention work timed on its own: per layer one RoPE + K/V
+    write + batched attention call (paged_rope_decode_attention, as the decode step makes
+    it) at the batch's final lengths, times the layers.
 
     Synthetic q/k/v/cos/sin of the step's shapes; layer 0's pool is written (after the
     timed steps, so nothing measured reads it).
     """
     import torch
 
-    from engine.kernels.paged_attention import paged_attention_decode_batched, pad_block_tables
-    from engine.kernels.paged_attention_integration import paged_rope_kv_write
+    from engine.kernels.paged_attention import pad_block_tables
+    from engine.kernels.paged_attention_integration import paged_rope_decode_attention
     from engine.workloads import QWEN25_05B as QWEN05
 
     b = len(seqs)
@@ -311,8 +312,7 @@ def attention_share_ms(dev, runner, seqs, iters=20):
     kc, vc = runner.pool.k_cache[0], runner.pool.v_cache[0]
 
     def layer():
-        qr = paged_rope_kv_write(q, k, v, cos, sin, kc, vc, tables, lens)
-        return paged_attention_decode_batched(qr, kc, vc, tables, lens, d ** -0.5)
+        return paged_rope_decode_attention(q, k, v, cos, sin, kc, vc, tables, lens, d ** -0.5)
 
     for _ in range(3):
         layer()

@@ -53,7 +53,8 @@ enum {
  * 4: pa_prefill_attention_f16; 5: its workspace; 6: pa_rmsnorm_f16, pa_silu_mul_f16;
  * 7: residual input of pa_rmsnorm_f16, pa_top2_f16; 8: pa_linear_f16; 9: pa_linear_f16
  * removed, decode workspace sizes stated per current device; 10:
- * pa_decode_batched_noalloc_f16). */
+ * pa_decode_batched_noalloc_f16; 11: pa_decode_rope_batched_f16, decode workspace
+ * with room for shared-prefix records). */
 PA_API int pa_abi_version(void);
 
 /* Message of the last failed call on this thread ("" after a success). */
@@ -195,6 +196,42 @@ PA_API int pa_rope_kv_write_f16(const void* q, const int64_t q_strides[3], const
                                 int uniform_seq_len, int num_seqs, int num_q_heads,
                                 int num_kv_heads, int head_dim, int block_size, int num_blocks,
                                 int max_blocks_per_seq, void* stream);
+
+/*
+ * One decode step's attention block of a layer in one call: the rotary
+ * embedding of the new token's q and key, the write of its rotated key and its
+ * value into the pool, and batched decode attention over L_b tokens. Replaces
+ * paged_decode_attention_forward's apply_rotary_pos_emb (engine/kernels/
+ * paged_attention_integration.py:108-109), its K/V write loop (:148-161) and its
+ * paged_attention_decode_batched call (:164-171). Results are the same bits as
+ * pa_rope_kv_write_f16 (same arguments, its q_out) followed by
+ * pa_decode_batched_f16 on the rotated queries; q, key, value, cos, sin, the
+ * caches, tables and lengths are as for those two calls, out as for the second.
+ * Batches that take one workgroup per (sequence, kv-head group) -- sequences x
+ * kv heads within the GPU's compute units, short tables -- at head_dim 64 or
+ * 128, block size 16 or 32, with 16-byte aligned unit-stride rows run as one
+ * kernel launch (the new rows are written at the end of the launch; the
+ * attention takes them from on-chip memory); all others as the two calls, with
+ * the rotated queries in the workspace. Workspace: at least
+ * pa_decode_rope_batched_workspace_bytes(), with the decode workspace's zeroed
+ * counter region at its start (same contract as pa_decode_batched_f16).
+ */
+PA_API size_t pa_decode_rope_batched_workspace_bytes(int num_seqs, int num_q_heads,
+                                                     int num_kv_heads, int head_dim,
+                                                     int block_size, int max_blocks_per_seq);
+PA_API int pa_decode_rope_batched_f16(const void* q, const int64_t q_strides[3], const void* key,
+                                      const int64_t key_strides[3], const void* value,
+                                      const int64_t value_strides[3], const void* cos,
+                                      const int64_t cos_strides[2], const void* sin,
+                                      const int64_t sin_strides[2], void* k_cache,
+                                      const int64_t k_strides[4], void* v_cache,
+                                      const int64_t v_strides[4], const int32_t* block_tables,
+                                      const int64_t bt_strides[2], const int32_t* seq_lens,
+                                      void* out, const int64_t out_strides[3], int num_seqs,
+                                      int num_q_heads, int num_kv_heads, int head_dim,
+                                      int block_size, int num_blocks, int max_blocks_per_seq,
+                                      float scale, void* workspace, size_t workspace_bytes,
+                                      void* stream);
 
 /*
  * Paged prefill attention: the new tokens of each sequence attend causally over

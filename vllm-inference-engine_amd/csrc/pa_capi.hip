@@ -312,7 +312,7 @@ using namespace pa;
 
 extern "C" {
 
-int pa_abi_version(void) { return 10; }
+int pa_abi_version(void) { return 11; }
 
 const char* pa_last_error(void) { return g_error.c_str(); }
 
@@ -792,6 +792,121 @@ int pa_rope_kv_write_f16(const void* q, const int64_t q_strides[3], const void* 
                    rows16(q_out, a.qo_b, a.qo_h, 1) && rows16(k_cache, a.kc_sb, a.kc_st, 1) &&
                    a.kc_sh % 8 == 0 && rows16(v_cache, a.vc_sb, a.vc_st, 1) && a.vc_sh % 8 == 0;
   return finish_launch(launch_rope_kv_write(a, vec, (hipStream_t)stream));
+}
+
+size_t pa_decode_rope_batched_workspace_bytes(int num_seqs, int num_q_heads, int num_kv_heads,
+                                              int head_dim, int block_size,
+                                              int max_blocks_per_seq) {
+  if (num_seqs <= 0 || num_q_heads <= 0 || num_kv_heads <= 0 || block_size <= 0 ||
+      max_blocks_per_seq <= 0 || !supported_head_dim(head_dim))
+    return 0;
+  // The decode workspace, then room for the rotated queries of the two-launch
+  // form (used when the one-launch kernel does not serve the shape).
+  const size_t ws = pa_decode_batched_workspace_bytes(num_seqs, num_q_heads, num_kv_heads,
+                                                      head_dim, block_size, max_blocks_per_seq);
+  return ((ws + 255) & ~(size_t)255) + (size_t)num_seqs * num_q_heads * head_dim * 2;
+}
+
+int pa_decode_rope_batched_f16(const void* q, const int64_t q_strides[3], const void* key,
+                               const int64_t key_strides[3], const void* value,
+                               const int64_t value_strides[3], const void* cos,
+                               const int64_t cos_strides[2], const void* sin,
+                               const int64_t sin_strides[2], void* k_cache,
+                               const int64_t k_strides[4], void* v_cache,
+                               const int64_t v_strides[4], const int32_t* block_tables,
+                               const int64_t bt_strides[2], const int32_t* seq_lens, void* out,
+                               const int64_t out_strides[3], int num_seqs, int num_q_heads,
+                               int num_kv_heads, int head_dim, int block_size, int num_blocks,
+                               int max_blocks_per_seq, float scale, void* workspace,
+                               size_t workspace_bytes, void* stream) {
+  clear_error();
+  if (num_seqs < 0) {
+    set_error("num_seqs must be >= 0");
+    return PA_ERR_ARG;
+  }
+  if (num_seqs == 0) return PA_OK;
+  if (!q || !key || !value || !cos || !sin || !k_cache || !v_cache || !out || !q_strides ||
+      !key_strides || !value_strides || !cos_strides || !sin_strides || !k_strides ||
+      !v_strides || !block_tables || !bt_strides || !seq_lens || !out_strides) {
+    set_error("null pointer argument");
+    return PA_ERR_ARG;
+  }
+  int rc = check_common(q, k_cache, v_cache, out, k_strides, v_strides, num_q_heads, num_kv_heads,
+                        head_dim, block_size, num_blocks);
+  if (rc) return rc;
+  const size_t ws_need = pa_decode_rope_batched_workspace_bytes(
+      num_seqs, num_q_heads, num_kv_heads, head_dim, block_size, max_blocks_per_seq);
+  if (!workspace || workspace_bytes < ws_need) {
+    set_error("workspace of %zu bytes needed, %zu given", ws_need, workspace_bytes);
+    return PA_ERR_WORKSPACE;
+  }
+  const size_t dec_ws = pa_decode_batched_workspace_bytes(num_seqs, num_q_heads, num_kv_heads,
+                                                          head_dim, block_size, max_blocks_per_seq);
+  // One launch when the batch takes one workgroup per (sequence, kv-head group)
+  // and every row the kernel reads with 16-byte loads is so aligned.
+  auto rows16 = [](const void* p, int64_t sb, int64_t sh, int64_t sd) {
+    return aligned(p, 16) && sd == 1 && sb % 8 == 0 && sh % 8 == 0;
+  };
+  DecodeArgs a{};
+  a.hkv = num_kv_heads;
+  a.g = num_q_heads / num_kv_heads;
+  a.bs = block_size;
+  a.max_blocks = max_blocks_per_seq;
+  a.k_st = k_strides[1];
+  a.k_sh = k_strides[2];
+  a.v_st = v_strides[1];
+  a.v_sh = v_strides[2];
+  streamk_plan(a, num_seqs, head_dim);
+  const bool one_launch =
+      num_seqs <= kSkMaxSeqs && pair_rope_supported(a, head_dim) &&
+      rows16(q, q_strides[0], q_strides[1], q_strides[2]) &&
+      rows16(key, key_strides[0], key_strides[1], key_strides[2]) &&
+      rows16(value, value_strides[0], value_strides[1], value_strides[2]) &&
+      rows16(cos, cos_strides[0], 0, cos_strides[1]) && rows16(sin, sin_strides[0], 0, sin_strides[1]) &&
+      out_strides[2] == 1 && out_strides[0] % 4 == 0 && out_strides[1] % 4 == 0;
+  if (!one_launch) {
+    // Two launches: rotation and K/V write, then attention on the rotated queries.
+    void* q_rot = (char*)workspace + ((dec_ws + 255) & ~(size_t)255);
+    const int64_t qr_strides[3] = {(int64_t)num_q_heads * head_dim, head_dim, 1};
+    rc = pa_rope_kv_write_f16(q, q_strides, key, key_strides, value, value_strides, cos, cos_strides,
+                              sin, sin_strides, q_rot, qr_strides, k_cache, k_strides, v_cache,
+                              v_strides, block_tables, bt_strides, seq_lens, 0, num_seqs,
+                              num_q_heads, num_kv_heads, head_dim, block_size, num_blocks,
+                              max_blocks_per_seq, stream);
+    if (rc) return rc;
+    return pa::decode_batched(q_rot, qr_strides, k_cache, k_strides, v_cache, v_strides,
+                              block_tables, bt_strides, seq_lens, out, out_strides, num_seqs,
+                              num_q_heads, num_kv_heads, head_dim, block_size, num_blocks,
+                              max_blocks_per_seq, scale, workspace, dec_ws, nullptr, stream);
+  }
+  a.q = (const f16*)q;
+  a.q_sb = q_strides[0];
+  a.q_sh = q_strides[1];
+  a.k = (const f16*)k_cache;
+  a.k_sb = k_strides[0];
+  a.v = (const f16*)v_cache;
+  a.v_sb = v_strides[0];
+  a.bt = block_tables;
+  a.bt_sb = bt_strides[0];
+  a.bt_sk = bt_strides[1];
+  a.lens = seq_lens;
+  a.out = (f16*)out;
+  a.o_sb = out_strides[0];
+  a.o_sh = out_strides[1];
+  a.num_blocks = num_blocks;
+  a.scale_log2 = scale * kLog2e;
+  RopeIn r{};
+  r.key = (const f16*)key;
+  r.ks_b = key_strides[0];
+  r.ks_h = key_strides[1];
+  r.val = (const f16*)value;
+  r.vs_b = value_strides[0];
+  r.vs_h = value_strides[1];
+  r.cos = (const f16*)cos;
+  r.cs_b = cos_strides[0];
+  r.sin = (const f16*)sin;
+  r.ss_b = sin_strides[0];
+  return finish_launch(launch_decode_pair_rope(a, r, head_dim, (hipStream_t)stream));
 }
 
 size_t pa_prefill_attention_workspace_bytes(int num_seqs, int num_q_heads, int num_kv_heads,

@@ -220,6 +220,26 @@ hipError_t launch_decode_streamk(const DecodeArgs& a, int D, hipStream_t s);
 // Whether the stream-K kernel launched for `a` builds prefix items (block size
 // 16 or 32, head_dim <= 64, pool strides its tile addressing covers).
 bool streamk_can_share(const DecodeArgs& a, int D);
+
+// The new token's rows of a fused decode-layer call (decode_pair_kernel with
+// rotary embedding): keys and values [num_seqs, kv heads, D] and the rotary
+// cos / sin rows [num_seqs, D], all with unit head_dim stride, 16-byte aligned
+// rows. Element strides.
+struct RopeIn {
+  const f16* key;
+  int64_t ks_b, ks_h;
+  const f16* val;
+  int64_t vs_b, vs_h;
+  const f16* cos;
+  int64_t cs_b;
+  const f16* sin;
+  int64_t ss_b;
+};
+// Whether the fused decode-layer kernel serves the launch planned in `a`
+// (one workgroup per pair, head_dim 64 or 128, block 16 or 32), and its
+// launcher.
+bool pair_rope_supported(const DecodeArgs& a, int D);
+hipError_t launch_decode_pair_rope(const DecodeArgs& a, const RopeIn& r, int D, hipStream_t s);
 hipError_t launch_prefill_attn(const PrefillAttnArgs& a, int D, hipStream_t s);
 hipError_t launch_rmsnorm(const f16* x, int64_t xs, const f16* res, int64_t rs, f16* sum,
                           int64_t ss, const f16* w, f16* y, int64_t ys, int rows, int H,

@@ -43,6 +43,14 @@ namespace pa {
 
 using namespace tiles;
 
+// Position of workgroup i among n in an order in which each XCD (workgroup i
+// runs on XCD i % 8) owns a contiguous run of positions.
+__device__ inline int xcd_order(int i, int n) {
+  const int n8 = n / kXcds, rem = n % kXcds;
+  const int xcd = i % kXcds, k = i / kXcds;
+  return xcd * n8 + (xcd < rem ? xcd : rem) + k;
+}
+
 // A wavefront-uniform value, moved to a scalar register.
 __device__ inline int uni(int v) { return __builtin_amdgcn_readfirstlane(v); }
 
@@ -105,13 +113,17 @@ __device__ inline int block_excl_sum(int (&v)[PER], int* s_tot, int lane, int wa
 // fragments qf[cb] with the K rows of kv head h0 + cb, or of kv head h0 for
 // every block when SHARED_K (a prefix item: all blocks belong to one kv head).
 // Only the first ncb blocks are computed (wavefront-uniform). The online
-// softmax state (exp2 domain) accumulates into m_run, l_run and acc.
+// softmax state (exp2 domain) accumulates into m_run, l_run and acc. With
+// nrow set (LDS: HGL rows of D halves for K, then HGL for V), the rows of
+// token npos are taken from nrow instead of the pool: a decode step's new
+// token, whose write into the pool need not have landed.
 template <int D, int BS, int HGL, int NCB, int NTL, bool SHARED_K, int NW>
 __device__ __forceinline__ void stream_tiles(const DecodeArgs& a, const int32_t* btrow, int h0,
                                              int s0, int s1, int L, int ncb,
                                              const f16x8 (&qf)[NCB][D / 32], f16* kst, f16* vst,
                                              int wave, int lane, float (&m_run)[NCB],
-                                             float (&l_run)[NCB], f32x4 (&acc)[NCB][D / 16]) {
+                                             float (&l_run)[NCB], f32x4 (&acc)[NCB][D / 16],
+                                             const f16* nrow = nullptr, int npos = -1) {
   constexpr int NC = D / 32;
   constexpr int ND = D / 16;
   constexpr int LS = D + 8;
@@ -198,7 +210,7 @@ __device__ __forceinline__ void stream_tiles(const DecodeArgs& a, const int32_t*
   };
   // Writes one tile's rows (natural layout) into the staging buffer laid out
   // [tile][head][row][LS]; rows past the sequence end are zeroed when asked.
-  auto stage = [&](int k, u32x4 (&buf)[NTL][NI], f16* dst, bool zero_tail) {
+  auto stage = [&](int k, u32x4 (&buf)[NTL][NI], f16* dst, bool zero_tail, int which) {
 #pragma unroll
     for (int nt = 0; nt < NTL; ++nt) {
       const int ti = s0 + k * NTL + nt;
@@ -225,6 +237,16 @@ __device__ __forceinline__ void stream_tiles(const DecodeArgs& a, const int32_t*
               *reinterpret_cast<f16x8*>(&dst[((nt * HGL + hg) * 16 + r) * LS + d0]) = zero8();
           }
         }
+        if (nrow != nullptr && ti == npos / 16) {  // wavefront-uniform
+          // The new token's rows replace what the pool held at its slot.
+          const int r = npos % 16;
+          for (int c = lane; c < HGL * D / 8; c += 64) {
+            const int hg = c / (D / 8);
+            const int d0 = (c - hg * (D / 8)) * 8;
+            *reinterpret_cast<f16x8*>(&dst[((nt * HGL + hg) * 16 + r) * LS + d0]) =
+                *reinterpret_cast<const f16x8*>(&nrow[(which * HGL + hg) * D + d0]);
+          }
+        }
       }
     }
   };
@@ -232,8 +254,8 @@ __device__ __forceinline__ void stream_tiles(const DecodeArgs& a, const int32_t*
   // Both K and V of chunk k go to LDS first, which frees their registers for
   // the loads of the chunk two steps ahead; the math then reads LDS only.
   auto stage_both = [&](int k, u32x4 (&kb)[NTL][NI], u32x4 (&vb)[NTL][NI]) {
-    stage(k, kb, kst, false);
-    stage(k, vb, vst, true);  // V rows past the sequence end as zeros: 0 * garbage is never NaN
+    stage(k, kb, kst, false, 0);
+    stage(k, vb, vst, true, 1);  // V rows past the sequence end as zeros: 0 * garbage is never NaN
     wave_lds_fence();
   };
   auto compute = [&](int k) {
@@ -669,31 +691,14 @@ void decode_streamk_kernel(DecodeArgs a) {
   const int Gw = (T + a.min_range - 1) / a.min_range;
   const int Ge = (int)(Gw < G ? Gw : G);  // 0 when every sequence is empty
 
-  // The first A workgroups take part. Workgroup i is dispatched to XCD i % 8;
-  // renumber the A of them so that each XCD owns a contiguous run of ranges
-  // (or pairs): neighbouring sequences then run on the same XCD and share its
-  // L2, and every XCD gets work when A < G.
-  const int A = a.pair_per_wg ? (B * NHG < G ? B * NHG : G) : Ge;
-  if ((int)blockIdx.x >= A) return;
-  const int wg = [&] {
-    const int n8 = A / kXcds, rem = A % kXcds;
-    const int xcd = blockIdx.x % kXcds, k = blockIdx.x / kXcds;
-    return xcd * n8 + (xcd < rem ? xcd : rem) + k;
-  }();
-  int x0, x1;
-  if (a.pair_per_wg) {
-    // Small batches of short pairs (no sharing): workgroup w takes pair w
-    // whole, so no pair is cut, no partial record is written and no merge is
-    // needed.
-    const int pb = wg / NHG;
-    const int width = (uni(s_pos[pb + 1]) - uni(s_pos[pb])) / NHG;
-    if (width == 0) return;  // a zero-length sequence: its rows were written above
-    x0 = uni(s_pos[pb]) + (wg - pb * NHG) * width;
-    x1 = x0 + width;
-  } else {
-    x0 = (int)range_start(wg, T, Ge);
-    x1 = (int)range_start(wg + 1, T, Ge);  // once per workgroup: 64-bit is fine
-  }
+  // The first Ge workgroups take part. Workgroup i is dispatched to XCD i % 8;
+  // renumber the Ge of them so that each XCD owns a contiguous run of ranges:
+  // neighbouring sequences then run on the same XCD and share its L2, and
+  // every XCD gets work when Ge < G.
+  if ((int)blockIdx.x >= Ge) return;
+  const int wg = xcd_order(blockIdx.x, Ge);
+  const int x0 = (int)range_start(wg, T, Ge);
+  const int x1 = (int)range_start(wg + 1, T, Ge);  // once per workgroup: 64-bit is fine
 
   // First item: in the last sequence whose items start at or before x0.
   int b;
@@ -1076,6 +1081,184 @@ void decode_streamk_kernel(DecodeArgs a) {
   resolve();
 }
 
+// Rotary embedding of the new token's q or key in fp16, op by op as
+// transformers' apply_rotary_pos_emb computes it (every product and sum
+// rounded on its own; no fused multiply-add): for element j of the first half
+// (x1, partner x2 = element j + D/2, cos and sin at j for o1 and at j + D/2
+// for o2)
+//   o1 = fp16(fp16(x1 * c1) + fp16(-x2 * s1)),  o2 = fp16(fp16(x2 * c2) + fp16(x1 * s2)).
+// The same statement as rope_kv_write_kernel, so both give the same bits. The
+// inputs are taken by value: the outputs may be the inputs' own variables.
+__device__ __forceinline__ void rope8(const f16x8 x1, const f16x8 x2, const f16x8 c1,
+                                      const f16x8 c2, const f16x8 s1, const f16x8 s2,
+                                      f16x8& o1, f16x8& o2) {
+#pragma clang fp contract(off)
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const f16 a1 = x1[e] * c1[e];
+    const f16 b1 = -(x2[e] * s1[e]);
+    o1[e] = a1 + b1;
+    const f16 a2 = x2[e] * c2[e];
+    const f16 b2 = x1[e] * s2[e];
+    o2[e] = a2 + b2;
+  }
+}
+
+// Batched decode with one workgroup per (sequence, kv-head group) pair, for
+// batches whose pairs fill the GPU and are short (the schedule the C API
+// picks for them): no plan and no partial records. Workgroup w takes pair w
+// (in XCD order); its first memory round trip brings the sequence's length,
+// the query rows and, with ROPE, the new token's key and value rows and the
+// rotary cos / sin rows.
+//
+// ROPE (the fused decode-layer form): q and the new key arrive unrotated;
+// the kernel rotates them (rope8), attends over the L tokens with the new
+// token's rotated key and value substituted for the pool's rows at position
+// L - 1, and writes them into that slot of the pool -- the work of
+// rope_kv_write_kernel followed by this kernel without it, in one launch. The
+// write is issued at the end: no workgroup but this one reads the pair's
+// rows during the launch.
+template <int D, int NT, int BS, int HG, int NW, bool ROPE>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void decode_pair_kernel(DecodeArgs a, RopeIn r) {
+  constexpr int NC = D / 32;
+  constexpr int ND = D / 16;
+  constexpr int LS = D + 8;
+  constexpr int VST = NT * HG * 16 * LS;
+  constexpr int CMB = 32 * HG + HG * ND * 64 * 4;
+  constexpr int WAVE_BYTES = 2 * VST * 2 > CMB * 4 ? 2 * VST * 2 : CMB * 4;
+  static_assert(!ROPE || D >= 64, "rotation pairs must lie in one lane's query fragments");
+  __shared__ __attribute__((aligned(16))) char smem[NW * WAVE_BYTES];
+  __shared__ __attribute__((aligned(16))) f16 s_new[ROPE ? 2 * HG * D : 8];  // new K rows, then V rows
+
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  const int row = lane & 15;
+  const int grp = lane >> 4;
+  const int NHG = a.hkv / HG;
+  const int P = a.num_seqs * NHG;
+  if ((int)blockIdx.x >= P) return;
+  const int wg = xcd_order(blockIdx.x, P);
+  const int b = wg / NHG;
+  const int h0 = (wg - b * NHG) * HG;
+  const int cap = a.max_blocks * a.bs;
+  const int L = min(max(a.lens ? load_uniform(a.lens + b) : a.uniform_len, 0), cap);
+
+  // Query fragments (rotated with ROPE: element j of the first half and its
+  // partner j + D / 2 sit in fragments c and c + NC / 2 of the same lane).
+  f16x8 qf[HG][NC];
+  {
+    const int gq = min(row, a.g - 1);
+#pragma unroll
+    for (int hg = 0; hg < HG; ++hg) {
+      const f16* qp = a.q + (int64_t)b * a.q_sb + (int64_t)((h0 + hg) * a.g + gq) * a.q_sh + grp * 8;
+#pragma unroll
+      for (int c = 0; c < NC; ++c) qf[hg][c] = *reinterpret_cast<const f16x8*>(qp + 32 * c);
+    }
+    if constexpr (ROPE) {
+      f16x8 cs[NC], sn[NC];
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        cs[c] = *reinterpret_cast<const f16x8*>(r.cos + (int64_t)b * r.cs_b + grp * 8 + 32 * c);
+        sn[c] = *reinterpret_cast<const f16x8*>(r.sin + (int64_t)b * r.ss_b + grp * 8 + 32 * c);
+      }
+#pragma unroll
+      for (int hg = 0; hg < HG; ++hg)
+#pragma unroll
+        for (int c = 0; c < NC / 2; ++c)
+          rope8(qf[hg][c], qf[hg][c + NC / 2], cs[c], cs[c + NC / 2], sn[c], sn[c + NC / 2],
+                qf[hg][c], qf[hg][c + NC / 2]);
+    }
+#pragma unroll
+    for (int hg = 0; hg < HG; ++hg)
+#pragma unroll
+      for (int c = 0; c < NC; ++c)
+        if (row >= a.g) qf[hg][c] = zero8();
+  }
+
+  // ROPE: the new token's rotated key and its value rows, into s_new. Lane
+  // t < HG * D / 16 of the first wavefront takes 8 elements j of one head and
+  // their partners j + D / 2.
+  constexpr int NRL = HG * D / 16;
+  if constexpr (ROPE) {
+    if (tid < NRL) {
+      const int hg = tid / (D / 16);
+      const int j = (tid - hg * (D / 16)) * 8;
+      const f16* kp = r.key + (int64_t)b * r.ks_b + (int64_t)(h0 + hg) * r.ks_h;
+      const f16* vp = r.val + (int64_t)b * r.vs_b + (int64_t)(h0 + hg) * r.vs_h;
+      const f16* cp = r.cos + (int64_t)b * r.cs_b;
+      const f16* sp = r.sin + (int64_t)b * r.ss_b;
+      f16x8 k1 = *reinterpret_cast<const f16x8*>(kp + j);
+      f16x8 k2 = *reinterpret_cast<const f16x8*>(kp + j + D / 2);
+      const f16x8 v1 = *reinterpret_cast<const f16x8*>(vp + j);
+      const f16x8 v2 = *reinterpret_cast<const f16x8*>(vp + j + D / 2);
+      rope8(k1, k2, *reinterpret_cast<const f16x8*>(cp + j), *reinterpret_cast<const f16x8*>(cp + j + D / 2),
+            *reinterpret_cast<const f16x8*>(sp + j), *reinterpret_cast<const f16x8*>(sp + j + D / 2), k1, k2);
+      *reinterpret_cast<f16x8*>(&s_new[hg * D + j]) = k1;
+      *reinterpret_cast<f16x8*>(&s_new[hg * D + j + D / 2]) = k2;
+      *reinterpret_cast<f16x8*>(&s_new[(HG + hg) * D + j]) = v1;
+      *reinterpret_cast<f16x8*>(&s_new[(HG + hg) * D + j + D / 2]) = v2;
+    }
+    __syncthreads();
+  }
+
+  if (L == 0) {  // no tokens: the rows are zeros (and nothing is written to the pool)
+    for (int i = tid; i < HG * a.g * D; i += 64 * NW) {
+      const int hq = i / D;
+      a.out[(int64_t)b * a.o_sb + (int64_t)(h0 * a.g + hq) * a.o_sh + (i - hq * D)] = (f16)0.f;
+    }
+    return;
+  }
+
+  f16* kst = reinterpret_cast<f16*>(smem + wave * WAVE_BYTES);
+  float m_run[HG], l_run[HG];
+  f32x4 acc[HG][ND];
+#pragma unroll
+  for (int hg = 0; hg < HG; ++hg) {
+    m_run[hg] = kNegInf;
+    l_run[hg] = 0.f;
+#pragma unroll
+    for (int i = 0; i < ND; ++i) acc[hg][i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  stream_tiles<D, BS, HG, HG, NT, false, NW>(a, a.bt + (int64_t)b * a.bt_sb, h0, 0, (L + 15) >> 4, L,
+                                             HG, qf, kst, kst + VST, wave, lane, m_run, l_run, acc,
+                                             ROPE ? s_new : nullptr, L - 1);
+  merge_waves<D, HG, NW>(smem, WAVE_BYTES, wave, lane, m_run, l_run, acc, HG,
+                         [&](int hg, int nd, float, float den, f32x4 num) {
+    if (row < a.g) {
+      const float inv = den > 0.f ? 1.f / den : 0.f;
+      f16x4 o;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) o[q] = (f16)(num[q] * inv);
+      *reinterpret_cast<f16x4*>(a.out + (int64_t)b * a.o_sb +
+                                (int64_t)((h0 + hg) * a.g + row) * a.o_sh + nd * 16 + grp * 4) = o;
+    }
+  });
+
+  if constexpr (ROPE) {
+    // The new token's slot: position L - 1, in the block the table lists for
+    // it; a slot outside the table or the pool is not written (as in
+    // rope_kv_write_kernel).
+    if (tid < NRL) {
+      const int pos = L - 1;
+      const int lb = pos / a.bs;
+      const int id = lb < a.max_blocks ? a.bt[(int64_t)b * a.bt_sb + (int64_t)lb * a.bt_sk] : -1;
+      if (id >= 0 && id < a.num_blocks) {
+        const int hg = tid / (D / 16);
+        const int j = (tid - hg * (D / 16)) * 8;
+        const int64_t off = (int64_t)(pos - lb * a.bs);
+        f16* kd = const_cast<f16*>(a.k) + (int64_t)id * a.k_sb + off * a.k_st + (int64_t)(h0 + hg) * a.k_sh;
+        f16* vd = const_cast<f16*>(a.v) + (int64_t)id * a.v_sb + off * a.v_st + (int64_t)(h0 + hg) * a.v_sh;
+        *reinterpret_cast<f16x8*>(kd + j) = *reinterpret_cast<const f16x8*>(&s_new[hg * D + j]);
+        *reinterpret_cast<f16x8*>(kd + j + D / 2) = *reinterpret_cast<const f16x8*>(&s_new[hg * D + j + D / 2]);
+        *reinterpret_cast<f16x8*>(vd + j) = *reinterpret_cast<const f16x8*>(&s_new[(HG + hg) * D + j]);
+        *reinterpret_cast<f16x8*>(vd + j + D / 2) = *reinterpret_cast<const f16x8*>(&s_new[(HG + hg) * D + j + D / 2]);
+      }
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Launchers.
 // ---------------------------------------------------------------------------
@@ -1093,7 +1276,17 @@ constexpr int sk_chunk_tiles(int hg) {
 template <int D, int BS, int HG>
 hipError_t launch_sk(const DecodeArgs& a, hipStream_t s) {
   constexpr int NT = sk_chunk_tiles<D>(HG);
-  decode_streamk_kernel<D, NT, BS, HG, kSkWaves><<<a.num_wg, 64 * kSkWaves, 0, s>>>(a);
+  if (a.pair_per_wg)
+    decode_pair_kernel<D, NT, BS, HG, kSkWaves, false><<<a.num_wg, 64 * kSkWaves, 0, s>>>(a, RopeIn{});
+  else
+    decode_streamk_kernel<D, NT, BS, HG, kSkWaves><<<a.num_wg, 64 * kSkWaves, 0, s>>>(a);
+  return hipGetLastError();
+}
+
+template <int D, int BS, int HG>
+hipError_t launch_pair_rope(const DecodeArgs& a, const RopeIn& r, hipStream_t s) {
+  constexpr int NT = sk_chunk_tiles<D>(HG);
+  decode_pair_kernel<D, NT, BS, HG, kSkWaves, true><<<a.num_wg, 64 * kSkWaves, 0, s>>>(a, r);
   return hipGetLastError();
 }
 
@@ -1124,6 +1317,21 @@ hipError_t launch_sk_bs(const DecodeArgs& a, hipStream_t s) {
 // host sizes the workspace and sets a.share only then).
 bool streamk_can_share(const DecodeArgs& a, int D) {
   return D <= 64 && (a.bs == 16 || a.bs == 32) && tile_offsets_fit(a, D, a.head_group);
+}
+
+bool pair_rope_supported(const DecodeArgs& a, int D) {
+  return a.pair_per_wg && (D == 64 || D == 128) && (a.bs == 16 || a.bs == 32) &&
+         tile_offsets_fit(a, D, a.head_group) && (a.head_group == 1 || D == 64);
+}
+
+hipError_t launch_decode_pair_rope(const DecodeArgs& a, const RopeIn& r, int D, hipStream_t s) {
+  if (!pair_rope_supported(a, D)) return hipErrorInvalidValue;
+  if (D == 64) {
+    if (a.head_group == 2)
+      return a.bs == 16 ? launch_pair_rope<64, 16, 2>(a, r, s) : launch_pair_rope<64, 32, 2>(a, r, s);
+    return a.bs == 16 ? launch_pair_rope<64, 16, 1>(a, r, s) : launch_pair_rope<64, 32, 1>(a, r, s);
+  }
+  return a.bs == 16 ? launch_pair_rope<128, 16, 1>(a, r, s) : launch_pair_rope<128, 32, 1>(a, r, s);
 }
 
 // Kv heads a wavefront handles together for this shape.

@@ -29,7 +29,7 @@ import logging
 import math
 from collections import OrderedDict
 from contextlib import contextmanager
-from typing import Any, Callable, List, Optional, Tuple, Union
+from typing import Any, Callable, Dict, List, Optional, Tuple, Union
 
 import numpy as np
 import torch
@@ -39,7 +39,6 @@ from . import _native
 from .paged_attention import (
     _on_device,
     pad_block_tables,
-    paged_attention_decode_batched,
     paged_attention_prefill,
 )
 
@@ -49,6 +48,7 @@ __all__ = [
     "PagedAttentionContext",
     "paged_kv_write",
     "paged_rope_kv_write",
+    "paged_rope_decode_attention",
     "paged_prefill_copy",
     "paged_decode_attention_forward",
     "paged_prefill_attention_forward",
@@ -205,6 +205,80 @@ def paged_rope_kv_write(
     return q_out
 
 
+_rope_ws_sizes: Dict[tuple, int] = {}
+
+
+def paged_rope_decode_attention(
+    query: torch.Tensor,         # [num_seqs, num_q_heads, (1,) head_dim] fp16, unrotated
+    key: torch.Tensor,           # [num_seqs, num_kv_heads, (1,) head_dim], unrotated
+    value: torch.Tensor,         # same as key
+    cos: torch.Tensor,           # [num_seqs, (1,) head_dim] fp16, the rotary table rows
+    sin: torch.Tensor,
+    k_cache: torch.Tensor,       # [num_blocks, block_size, num_kv_heads, head_dim] fp16
+    v_cache: torch.Tensor,
+    block_tables: torch.Tensor,  # [num_seqs, max_blocks_per_seq] int32
+    seq_lens: torch.Tensor,      # [num_seqs] int32, lengths including the new token
+    scale: float,
+) -> torch.Tensor:
+    """One decode step's attention block of a layer, in one call.
+
+    The same bits as paged_rope_kv_write(query, key, value, cos, sin, k_cache,
+    v_cache, block_tables, seq_lens) followed by paged_attention_decode_batched
+    on the rotated queries -- the reference's apply_rotary_pos_emb
+    (integration.py:108-109), K/V write loop (:148-161) and batched attention
+    call (:164-171). Batches that take one workgroup per (sequence, kv-head
+    group) pair run as one kernel launch; the others as those two launches.
+    Returns [num_seqs, num_q_heads, head_dim]; asynchronous on the current stream.
+    """
+    query = _as_rows(query)
+    key = _as_rows(key)
+    value = _as_rows(value)
+    cos = _rope_rows(cos)
+    sin = _rope_rows(sin)
+    for t in (query, key, value, cos, sin, k_cache, v_cache):
+        assert t.is_cuda and t.dtype == torch.float16
+    assert block_tables.dtype == torch.int32 and block_tables.is_cuda and block_tables.dim() == 2
+    assert seq_lens.is_cuda and seq_lens.dtype == torch.int32
+    _native.same_device(query, key, value, cos, sin, k_cache, v_cache, block_tables, seq_lens)
+    assert k_cache.shape == v_cache.shape, "k_cache and v_cache must have the same shape"
+    num_blocks, block_size, num_kv_heads, head_dim = k_cache.shape
+    num_seqs, num_q_heads = query.shape[0], query.shape[1]
+    assert query.shape[2] == head_dim and head_dim % 2 == 0
+    assert num_q_heads % num_kv_heads == 0, (
+        f"num_q_heads ({num_q_heads}) must be divisible by num_kv_heads ({num_kv_heads})")
+    assert key.shape == (num_seqs, num_kv_heads, head_dim) and value.shape == key.shape
+    assert cos.shape == (num_seqs, head_dim) and sin.shape == cos.shape
+    assert block_tables.shape[0] == num_seqs and seq_lens.shape == (num_seqs,)
+    out = torch.empty((num_seqs, num_q_heads, head_dim), dtype=torch.float16, device=query.device)
+    if num_seqs == 0:
+        return out
+    lib = _native.load()
+    dev = query.device
+    max_blocks = block_tables.shape[1]
+    ws_key = (dev.index, num_seqs, num_q_heads, num_kv_heads, head_dim, block_size, max_blocks)
+    stream = _native.stream_handle(dev)
+    with _on_device(dev):
+        ws_bytes = _rope_ws_sizes.get(ws_key)
+        if ws_bytes is None:
+            ws_bytes = _rope_ws_sizes[ws_key] = lib.pa_decode_rope_batched_workspace_bytes(
+                *ws_key[1:])
+        status = lib.pa_decode_rope_batched_f16(
+            query.data_ptr(), _native.strides_of(query),
+            key.data_ptr(), _native.strides_of(key),
+            value.data_ptr(), _native.strides_of(value),
+            cos.data_ptr(), _native.strides_of(cos),
+            sin.data_ptr(), _native.strides_of(sin),
+            k_cache.data_ptr(), _native.strides_of(k_cache),
+            v_cache.data_ptr(), _native.strides_of(v_cache),
+            block_tables.data_ptr(), _native.strides_of(block_tables),
+            seq_lens.data_ptr(), out.data_ptr(), _native.strides_of(out),
+            num_seqs, num_q_heads, num_kv_heads, head_dim, block_size, num_blocks, max_blocks,
+            float(scale), _native.workspace(ws_bytes, dev, stream, _native.WS_DECODE), ws_bytes,
+            stream)
+    _native.check(status, "pa_decode_rope_batched_f16")
+    return out
+
+
 class PagedAttentionContext:
     """Per-step metadata handed to the patched attention modules (reference integration.py:29-62).
 
@@ -293,11 +367,11 @@ def paged_decode_attention_forward(
 ) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
     """Drop-in Qwen2Attention.forward for one decode step (reference integration.py:65-176).
 
-    q/k/v projections; RoPE of q and k together with the new K/V's write into
-    the pool in one paged_rope_kv_write launch (bit-identical to transformers'
-    apply_rotary_pos_emb followed by the reference's write loop); batched paged
-    attention over L_b tokens (the write precedes the read, as in the
-    reference); then o_proj.
+    q/k/v projections; then paged_rope_decode_attention: RoPE of q and k, the
+    new K/V's write into the pool (bit-identical to transformers'
+    apply_rotary_pos_emb followed by the reference's write loop) and batched
+    paged attention over L_b tokens (the write precedes the read, as in the
+    reference), in one launch where the batch allows; then o_proj.
     """
     ctx: Optional[PagedAttentionContext] = getattr(self, "_paged_attention_context", None)
     if ctx is not None and getattr(ctx, "is_prefill", False):
@@ -331,26 +405,16 @@ def paged_decode_attention_forward(
     v_cache = pool.v_cache[layer_idx]
 
     if not ctx.is_batched:
-        bt = ctx.block_table_tensor
-        seq_len = ctx.single_seq_len
-        q_rot = paged_rope_kv_write(query_states, key_states, value_states, cos, sin,
-                                    k_cache, v_cache, bt, seq_len)
-        seq_lens_t = torch.tensor([seq_len], dtype=torch.int32, device=pool.device)
-        bt_2d = bt.unsqueeze(0)
+        bt_2d = ctx.block_table_tensor.unsqueeze(0)
+        seq_lens_t = torch.tensor([ctx.single_seq_len], dtype=torch.int32, device=pool.device)
     else:
         bt_2d = ctx.padded_block_tables
         seq_lens_t = ctx.seq_lens_tensor
-        q_rot = paged_rope_kv_write(query_states, key_states, value_states, cos, sin,
-                                    k_cache, v_cache, bt_2d, seq_lens_t)
 
-    attn_output = paged_attention_decode_batched(
-        q=q_rot,
-        k_cache=k_cache,
-        v_cache=v_cache,
-        block_tables=bt_2d,
-        seq_lens=seq_lens_t,
-        scale=scale,
-    )
+    # RoPE of q and k, the write of the new K/V into the pool, then attention
+    # over L_b tokens (the write precedes the read, as in the reference).
+    attn_output = paged_rope_decode_attention(query_states, key_states, value_states, cos, sin,
+                                              k_cache, v_cache, bt_2d, seq_lens_t, scale)
     attn_output = attn_output.reshape(*input_shape, -1).contiguous()
     attn_output = self.o_proj(attn_output)
     return attn_output, None
@@ -560,8 +624,7 @@ def fused_decoder_layer_forward(
     else:
         bt_2d = ctx.block_table_tensor.unsqueeze(0)
         lens = torch.tensor([ctx.single_seq_len], dtype=torch.int32, device=ctx.pool.device)
-    q_rot = paged_rope_kv_write(q, k, v, cos, sin, k_cache, v_cache, bt_2d, lens)
-    o = paged_attention_decode_batched(q_rot, k_cache, v_cache, bt_2d, lens, scale)
+    o = paged_rope_decode_attention(q, k, v, cos, sin, k_cache, v_cache, bt_2d, lens, scale)
     proj = torch.nn.functional.linear(o.reshape(b, nq * hd), attn.o_proj.weight, attn.o_proj.bias)
     h, hn = rms_norm(proj, self.post_attention_layernorm.weight,
                      self.post_attention_layernorm.variance_epsilon, residual=x)
