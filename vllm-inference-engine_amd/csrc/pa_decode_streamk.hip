@@ -107,7 +107,9 @@ __device__ inline int block_excl_sum(int (&v)[PER], int* s_tot, int lane, int wa
 }
 
 // One wavefront's share of an item segment: tiles s0 .. s1 - 1 (token rows
-// 16 ti .. 16 ti + 15 of the sequence whose table row is btrow, length L) of
+// 16 ti .. 16 ti + 15 of the sequence whose table row is btrow, length L;
+// {s1, L} = seg(), called once the first chunks' block ids are issued where a
+// tile lies in one block, so that a length loaded there shares their wait) of
 // kv heads h0 .. h0 + HGL - 1, in chunks of NTL tiles w, w + NW, ... (w the
 // wavefront). Column block cb of the 16 x 16 score tiles multiplies the query
 // fragments qf[cb] with the K rows of kv head h0 + cb, or of kv head h0 for
@@ -115,15 +117,31 @@ __device__ inline int block_excl_sum(int (&v)[PER], int* s_tot, int lane, int wa
 // Only the first ncb blocks are computed (wavefront-uniform). The online
 // softmax state (exp2 domain) accumulates into m_run, l_run and acc. With
 // nrow set (LDS: HGL rows of D halves for K, then HGL for V), the rows of
-// token npos are taken from nrow instead of the pool: a decode step's new
-// token, whose write into the pool need not have landed.
-template <int D, int BS, int HGL, int NCB, int NTL, bool SHARED_K, int NW>
+// token L - 1 are taken from nrow instead of the pool: a decode step's new
+// token, whose write into the pool need not have landed. pre_loop() runs in
+// every wavefront after the first chunks' loads are issued, before any is
+// staged or computed (nrow and qf must be complete when it returns).
+struct SegEnd {
+  int s1, L;
+};
+struct KnownSeg {
+  static constexpr bool kLoads = false;
+  int s1, L;
+  __device__ SegEnd operator()() const { return {s1, L}; }
+};
+struct NoPreLoop {
+  __device__ void operator()() const {}
+};
+
+template <int D, int BS, int HGL, int NCB, int NTL, bool SHARED_K, int NW, typename Seg,
+          typename PreLoop = NoPreLoop>
 __device__ __forceinline__ void stream_tiles(const DecodeArgs& a, const int32_t* btrow, int h0,
-                                             int s0, int s1, int L, int ncb,
+                                             int s0, Seg seg, int ncb,
                                              const f16x8 (&qf)[NCB][D / 32], f16* kst, f16* vst,
                                              int wave, int lane, float (&m_run)[NCB],
                                              float (&l_run)[NCB], f32x4 (&acc)[NCB][D / 16],
-                                             const f16* nrow = nullptr, int npos = -1) {
+                                             const f16* nrow = nullptr,
+                                             PreLoop pre_loop = PreLoop{}) {
   constexpr int NC = D / 32;
   constexpr int ND = D / 16;
   constexpr int LS = D + 8;
@@ -140,7 +158,15 @@ __device__ __forceinline__ void stream_tiles(const DecodeArgs& a, const int32_t*
   const int row = lane & 15;
   const int grp = lane >> 4;
   const int bs = BS > 0 ? BS : a.bs;
+  h0 = uni(h0);  // keeps the tile resources in scalar registers
+  int s1 = 0, L = 0;
+  if constexpr (!UNIFORM_TILE) {  // the rows' block ids need the length
+    const SegEnd e = seg();
+    s1 = e.s1;
+    L = e.L;
+  }
   const int tok_fallback = s0 * 16;  // a valid token of this segment
+  const int last_tile = a.max_blocks * (bs / 16) - 1;  // the table's last 16-token tile (uniform tiles)
 
   // Byte offset of this lane's 16-byte piece within a tile, relative to the
   // tile's first row at the first loaded kv head (same for every tile).
@@ -169,11 +195,16 @@ __device__ __forceinline__ void stream_tiles(const DecodeArgs& a, const int32_t*
       for (int j = 0; j < NID; ++j) {
         // A uniform tile lies in one block; otherwise each lane looks up the
         // block of its own row (also when one instruction covers the tile).
-        const int t = row_token(s0 + k * NTL + nt, UNIFORM_TILE ? 0 : nat_row(j));
-        if constexpr (UNIFORM_TILE)
-          ids[nt][j] = load_uniform(btrow + (int64_t)blk_of<BS>(t, bs) * a.bt_sk);
-        else
+        if constexpr (UNIFORM_TILE) {
+          // The tile's entry, clamped to the table width only: no dependence on
+          // the length, so the first ids can be in flight with the length
+          // itself (a tile past the segment gets an empty resource anyway).
+          const int ti = min(s0 + k * NTL + nt, last_tile);
+          ids[nt][j] = load_uniform(btrow + (int64_t)(ti / (BS / 16)) * a.bt_sk);
+        } else {
+          const int t = row_token(s0 + k * NTL + nt, nat_row(j));
           ids[nt][j] = btrow[(int64_t)blk_of<BS>(t, bs) * a.bt_sk];
+        }
       }
   };
   auto load_kv = [&](int k, const int (&ids)[NTL][NID], u32x4 (&kb)[NTL][NI],
@@ -237,9 +268,9 @@ __device__ __forceinline__ void stream_tiles(const DecodeArgs& a, const int32_t*
               *reinterpret_cast<f16x8*>(&dst[((nt * HGL + hg) * 16 + r) * LS + d0]) = zero8();
           }
         }
-        if (nrow != nullptr && ti == npos / 16) {  // wavefront-uniform
+        if (nrow != nullptr && L > 0 && ti == (L - 1) / 16) {  // wavefront-uniform
           // The new token's rows replace what the pool held at its slot.
-          const int r = npos % 16;
+          const int r = (L - 1) % 16;
           for (int c = lane; c < HGL * D / 8; c += 64) {
             const int hg = c / (D / 8);
             const int d0 = (c - hg * (D / 8)) * 8;
@@ -370,7 +401,6 @@ __device__ __forceinline__ void stream_tiles(const DecodeArgs& a, const int32_t*
   // then compute step s. Claims are increasing per wavefront, so the first
   // claim past the end ends its work; loads of such chunks are issued anyway
   // (empty resources, clamped table reads) so that no branch separates them.
-  const int nck = __builtin_amdgcn_readfirstlane((s1 - s0 + NTL - 1) / NTL);
   int next_chunk = wave;
   auto claim = [&]() {
     const int c = next_chunk;
@@ -384,6 +414,16 @@ __device__ __forceinline__ void stream_tiles(const DecodeArgs& a, const int32_t*
   int c2 = claim();
   load_ids(c0, ids0);
   load_ids(c1, ids1);
+  if constexpr (UNIFORM_TILE) {
+    // Everything issued so far is in flight before the first use of the
+    // length: the block ids and a length that seg() loads share one wait.
+    if constexpr (Seg::kLoads) __builtin_amdgcn_sched_barrier(0);
+    const SegEnd e = seg();
+    if constexpr (Seg::kLoads) __builtin_amdgcn_sched_barrier(0);
+    s1 = e.s1;
+    L = e.L;
+  }
+  const int nck = __builtin_amdgcn_readfirstlane((s1 - s0 + NTL - 1) / NTL);
   // The scheduler must keep the loads of step 0 ahead of those of step 1:
   // the loop's waits count on the older buffer being the one staged first.
   load_kv(c0, ids0, kb0, vb0);
@@ -391,6 +431,9 @@ __device__ __forceinline__ void stream_tiles(const DecodeArgs& a, const int32_t*
   load_kv(c1, ids1, kb1, vb1);
   __builtin_amdgcn_sched_barrier(0);
   load_ids(c2, ids0);
+  // The caller's work that may run once the first loads are in flight (every
+  // wavefront calls it; it may hold a barrier).
+  pre_loop();
   // Two steps per trip, one exit: both steps issue their loads on every trip
   // and only the LDS staging and the math of a step past the end are skipped,
   // so every path through the loop issues the same loads.
@@ -981,8 +1024,9 @@ void decode_streamk_kernel(DecodeArgs a) {
 #pragma unroll
         for (int i = 0; i < ND; ++i) acc[hg][i] = f32x4{0.f, 0.f, 0.f, 0.f};
       }
-      stream_tiles<D, BS, HG, HG, NT, false, NW>(a, a.bt + (int64_t)b * a.bt_sb, h0, s0, s1, L, HG,
-                                                 qf, kst, kst + VST, wave, lane, m_run, l_run, acc);
+      stream_tiles<D, BS, HG, HG, NT, false, NW>(a, a.bt + (int64_t)b * a.bt_sb, h0, s0,
+                                                 KnownSeg{s1, L}, HG, qf, kst, kst + VST, wave,
+                                                 lane, m_run, l_run, acc);
       const bool final_out = whole && g.pt == 0;
       merge_waves<D, HG, NW>(smem, WAVE_BYTES, wave, lane, m_run, l_run, acc, HG,
                              [&](int hg, int nd, float M, float den, f32x4 num) {
@@ -1048,9 +1092,9 @@ void decode_streamk_kernel(DecodeArgs a) {
 #pragma unroll
           for (int i = 0; i < ND; ++i) acc[cb][i] = f32x4{0.f, 0.f, 0.f, 0.f};
         }
-        stream_tiles<D, BS, 1, NCP, NTP, true, NW>(a, a.bt + (int64_t)b * a.bt_sb, h, s0, s1, L,
-                                                   ncb, qf, kst, kst + VSTP, wave, lane, m_run,
-                                                   l_run, acc);
+        stream_tiles<D, BS, 1, NCP, NTP, true, NW>(a, a.bt + (int64_t)b * a.bt_sb, h, s0,
+                                                   KnownSeg{s1, L}, ncb, qf, kst, kst + VSTP, wave,
+                                                   lane, m_run, l_run, acc);
         merge_waves<D, NCP, NW>(smem, WAVE_BYTES, wave, lane, m_run, l_run, acc, ncb,
                                 [&](int cb, int nd, float M, float den, f32x4 num) {
           // Column block cb is one record: row = column (member, query head).
@@ -1104,12 +1148,26 @@ __device__ __forceinline__ void rope8(const f16x8 x1, const f16x8 x2, const f16x
   }
 }
 
+// The pair kernel's segment end: the whole sequence, its length loaded where
+// stream_tiles asks for it (and kept in L_out for the rest of the kernel).
+struct PairSeg {
+  static constexpr bool kLoads = true;
+  const int32_t* len;  // nullptr: every sequence has uniform_len tokens
+  int uniform_len, cap;
+  int& L_out;
+  __device__ SegEnd operator()() const {
+    const int L = min(max(len ? load_uniform(len) : uniform_len, 0), cap);
+    L_out = L;
+    return {(L + 15) >> 4, L};
+  }
+};
+
 // Batched decode with one workgroup per (sequence, kv-head group) pair, for
 // batches whose pairs fill the GPU and are short (the schedule the C API
 // picks for them): no plan and no partial records. Workgroup w takes pair w
 // (in XCD order); its first memory round trip brings the sequence's length,
-// the query rows and, with ROPE, the new token's key and value rows and the
-// rotary cos / sin rows.
+// the block ids of its first chunks, the query rows and, with ROPE, the new
+// token's key and value rows and the rotary cos / sin rows.
 //
 // ROPE (the fused decode-layer form): q and the new key arrive unrotated;
 // the kernel rotates them (rope8), attends over the L tokens with the new
@@ -1142,12 +1200,12 @@ void decode_pair_kernel(DecodeArgs a, RopeIn r) {
   const int wg = xcd_order(blockIdx.x, P);
   const int b = wg / NHG;
   const int h0 = (wg - b * NHG) * HG;
-  const int cap = a.max_blocks * a.bs;
-  const int L = min(max(a.lens ? load_uniform(a.lens + b) : a.uniform_len, 0), cap);
 
-  // Query fragments (rotated with ROPE: element j of the first half and its
-  // partner j + D / 2 sit in fragments c and c + NC / 2 of the same lane).
+  // Query fragments (with ROPE, element j of the first half and its partner
+  // j + D / 2 sit in fragments c and c + NC / 2 of the same lane). Only their
+  // loads are issued here; the rotation waits for the pipeline's first loads.
   f16x8 qf[HG][NC];
+  f16x8 qc[ROPE ? NC : 1], qs[ROPE ? NC : 1];
   {
     const int gq = min(row, a.g - 1);
 #pragma unroll
@@ -1157,30 +1215,25 @@ void decode_pair_kernel(DecodeArgs a, RopeIn r) {
       for (int c = 0; c < NC; ++c) qf[hg][c] = *reinterpret_cast<const f16x8*>(qp + 32 * c);
     }
     if constexpr (ROPE) {
-      f16x8 cs[NC], sn[NC];
 #pragma unroll
       for (int c = 0; c < NC; ++c) {
-        cs[c] = *reinterpret_cast<const f16x8*>(r.cos + (int64_t)b * r.cs_b + grp * 8 + 32 * c);
-        sn[c] = *reinterpret_cast<const f16x8*>(r.sin + (int64_t)b * r.ss_b + grp * 8 + 32 * c);
+        qc[c] = *reinterpret_cast<const f16x8*>(r.cos + (int64_t)b * r.cs_b + grp * 8 + 32 * c);
+        qs[c] = *reinterpret_cast<const f16x8*>(r.sin + (int64_t)b * r.ss_b + grp * 8 + 32 * c);
       }
+    } else {
 #pragma unroll
       for (int hg = 0; hg < HG; ++hg)
 #pragma unroll
-        for (int c = 0; c < NC / 2; ++c)
-          rope8(qf[hg][c], qf[hg][c + NC / 2], cs[c], cs[c + NC / 2], sn[c], sn[c + NC / 2],
-                qf[hg][c], qf[hg][c + NC / 2]);
+        for (int c = 0; c < NC; ++c)
+          if (row >= a.g) qf[hg][c] = zero8();
     }
-#pragma unroll
-    for (int hg = 0; hg < HG; ++hg)
-#pragma unroll
-      for (int c = 0; c < NC; ++c)
-        if (row >= a.g) qf[hg][c] = zero8();
   }
 
-  // ROPE: the new token's rotated key and its value rows, into s_new. Lane
-  // t < HG * D / 16 of the first wavefront takes 8 elements j of one head and
-  // their partners j + D / 2.
+  // ROPE: the new token's key and value rows. Lane t < HG * D / 16 of the
+  // first wavefront takes 8 elements j of one head and their partners
+  // j + D / 2; the rotated key and the value go to s_new.
   constexpr int NRL = HG * D / 16;
+  f16x8 nk1, nk2, nv1, nv2, nc1, nc2, ns1, ns2;
   if constexpr (ROPE) {
     if (tid < NRL) {
       const int hg = tid / (D / 16);
@@ -1189,27 +1242,48 @@ void decode_pair_kernel(DecodeArgs a, RopeIn r) {
       const f16* vp = r.val + (int64_t)b * r.vs_b + (int64_t)(h0 + hg) * r.vs_h;
       const f16* cp = r.cos + (int64_t)b * r.cs_b;
       const f16* sp = r.sin + (int64_t)b * r.ss_b;
-      f16x8 k1 = *reinterpret_cast<const f16x8*>(kp + j);
-      f16x8 k2 = *reinterpret_cast<const f16x8*>(kp + j + D / 2);
-      const f16x8 v1 = *reinterpret_cast<const f16x8*>(vp + j);
-      const f16x8 v2 = *reinterpret_cast<const f16x8*>(vp + j + D / 2);
-      rope8(k1, k2, *reinterpret_cast<const f16x8*>(cp + j), *reinterpret_cast<const f16x8*>(cp + j + D / 2),
-            *reinterpret_cast<const f16x8*>(sp + j), *reinterpret_cast<const f16x8*>(sp + j + D / 2), k1, k2);
-      *reinterpret_cast<f16x8*>(&s_new[hg * D + j]) = k1;
-      *reinterpret_cast<f16x8*>(&s_new[hg * D + j + D / 2]) = k2;
-      *reinterpret_cast<f16x8*>(&s_new[(HG + hg) * D + j]) = v1;
-      *reinterpret_cast<f16x8*>(&s_new[(HG + hg) * D + j + D / 2]) = v2;
+      nk1 = *reinterpret_cast<const f16x8*>(kp + j);
+      nk2 = *reinterpret_cast<const f16x8*>(kp + j + D / 2);
+      nv1 = *reinterpret_cast<const f16x8*>(vp + j);
+      nv2 = *reinterpret_cast<const f16x8*>(vp + j + D / 2);
+      nc1 = *reinterpret_cast<const f16x8*>(cp + j);
+      nc2 = *reinterpret_cast<const f16x8*>(cp + j + D / 2);
+      ns1 = *reinterpret_cast<const f16x8*>(sp + j);
+      ns2 = *reinterpret_cast<const f16x8*>(sp + j + D / 2);
     }
-    __syncthreads();
   }
+  // Runs in every wavefront once the first chunks' loads are in flight.
+  auto rotate = [&]() {
+    if constexpr (ROPE) {
+#pragma unroll
+      for (int hg = 0; hg < HG; ++hg) {
+#pragma unroll
+        for (int c = 0; c < NC / 2; ++c)
+          rope8(qf[hg][c], qf[hg][c + NC / 2], qc[c], qc[c + NC / 2], qs[c], qs[c + NC / 2],
+                qf[hg][c], qf[hg][c + NC / 2]);
+#pragma unroll
+        for (int c = 0; c < NC; ++c)
+          if (row >= a.g) qf[hg][c] = zero8();
+      }
+      if (tid < NRL) {
+        const int hg = tid / (D / 16);
+        const int j = (tid - hg * (D / 16)) * 8;
+        rope8(nk1, nk2, nc1, nc2, ns1, ns2, nk1, nk2);
+        *reinterpret_cast<f16x8*>(&s_new[hg * D + j]) = nk1;
+        *reinterpret_cast<f16x8*>(&s_new[hg * D + j + D / 2]) = nk2;
+        *reinterpret_cast<f16x8*>(&s_new[(HG + hg) * D + j]) = nv1;
+        *reinterpret_cast<f16x8*>(&s_new[(HG + hg) * D + j + D / 2]) = nv2;
+      }
+      __syncthreads();
+    }
+  };
 
-  if (L == 0) {  // no tokens: the rows are zeros (and nothing is written to the pool)
-    for (int i = tid; i < HG * a.g * D; i += 64 * NW) {
-      const int hq = i / D;
-      a.out[(int64_t)b * a.o_sb + (int64_t)(h0 * a.g + hq) * a.o_sh + (i - hq * D)] = (f16)0.f;
-    }
-    return;
-  }
+  // The length is loaded after the first block ids are issued (they do not
+  // depend on it), so that both arrive in one round trip. A sequence with no
+  // tokens streams no tile: every wavefront keeps an empty state and the
+  // merge writes rows of zeros.
+  int L = 0;
+  PairSeg seg{a.lens ? a.lens + b : nullptr, a.uniform_len, a.max_blocks * a.bs, L};
 
   f16* kst = reinterpret_cast<f16*>(smem + wave * WAVE_BYTES);
   float m_run[HG], l_run[HG];
@@ -1221,9 +1295,9 @@ void decode_pair_kernel(DecodeArgs a, RopeIn r) {
 #pragma unroll
     for (int i = 0; i < ND; ++i) acc[hg][i] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
-  stream_tiles<D, BS, HG, HG, NT, false, NW>(a, a.bt + (int64_t)b * a.bt_sb, h0, 0, (L + 15) >> 4, L,
-                                             HG, qf, kst, kst + VST, wave, lane, m_run, l_run, acc,
-                                             ROPE ? s_new : nullptr, L - 1);
+  stream_tiles<D, BS, HG, HG, NT, false, NW>(a, a.bt + (int64_t)b * a.bt_sb, h0, 0, seg, HG, qf,
+                                             kst, kst + VST, wave, lane, m_run, l_run, acc,
+                                             ROPE ? s_new : nullptr, rotate);
   merge_waves<D, HG, NW>(smem, WAVE_BYTES, wave, lane, m_run, l_run, acc, HG,
                          [&](int hg, int nd, float, float den, f32x4 num) {
     if (row < a.g) {
@@ -1239,8 +1313,8 @@ void decode_pair_kernel(DecodeArgs a, RopeIn r) {
   if constexpr (ROPE) {
     // The new token's slot: position L - 1, in the block the table lists for
     // it; a slot outside the table or the pool is not written (as in
-    // rope_kv_write_kernel).
-    if (tid < NRL) {
+    // rope_kv_write_kernel), nor is anything for a sequence with no tokens.
+    if (tid < NRL && L > 0) {
       const int pos = L - 1;
       const int lb = pos / a.bs;
       const int id = lb < a.max_blocks ? a.bt[(int64_t)b * a.bt_sb + (int64_t)lb * a.bt_sk] : -1;
