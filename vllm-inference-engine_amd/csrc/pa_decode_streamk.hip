@@ -471,8 +471,9 @@ __device__ __forceinline__ void merge_waves(char* smem, int wave_bytes, int wave
   constexpr int ND = D / 16;
   const int row = lane & 15;
   const int grp = lane >> 4;
+  // A wavefront's state goes to its own area, which held only its own
+  // staging buffers: no barrier is needed before these writes.
   float* cm = reinterpret_cast<float*>(smem + wave * wave_bytes);
-  __syncthreads();  // every wavefront is done with its staging buffers
 #pragma unroll
   for (int cb = 0; cb < NCB; ++cb) {
     if (cb < ncb) {
@@ -1252,9 +1253,20 @@ void decode_pair_kernel(DecodeArgs a, RopeIn r) {
       ns2 = *reinterpret_cast<const f16x8*>(sp + j + D / 2);
     }
   }
-  // Runs in every wavefront once the first chunks' loads are in flight.
+  // The length is loaded after the first block ids are issued (they do not
+  // depend on it), so that both arrive in one round trip. A sequence with no
+  // tokens streams no tile: every wavefront keeps an empty state and the
+  // merge writes rows of zeros.
+  int L = 0;
+  // Runs in every wavefront once the first chunks' loads are in flight (the
+  // length known): with ROPE it also fetches the block id of the new token's
+  // slot, position L - 1, for the write at the end.
+  int slot_id = -1;
   auto rotate = [&]() {
     if constexpr (ROPE) {
+      const int lb = (L - 1) / a.bs;
+      if (L > 0 && lb < a.max_blocks)
+        slot_id = load_uniform(a.bt + (int64_t)b * a.bt_sb + (int64_t)lb * a.bt_sk);
 #pragma unroll
       for (int hg = 0; hg < HG; ++hg) {
 #pragma unroll
@@ -1278,11 +1290,6 @@ void decode_pair_kernel(DecodeArgs a, RopeIn r) {
     }
   };
 
-  // The length is loaded after the first block ids are issued (they do not
-  // depend on it), so that both arrive in one round trip. A sequence with no
-  // tokens streams no tile: every wavefront keeps an empty state and the
-  // merge writes rows of zeros.
-  int L = 0;
   PairSeg seg{a.lens ? a.lens + b : nullptr, a.uniform_len, a.max_blocks * a.bs, L};
 
   f16* kst = reinterpret_cast<f16*>(smem + wave * WAVE_BYTES);
@@ -1317,7 +1324,7 @@ void decode_pair_kernel(DecodeArgs a, RopeIn r) {
     if (tid < NRL && L > 0) {
       const int pos = L - 1;
       const int lb = pos / a.bs;
-      const int id = lb < a.max_blocks ? a.bt[(int64_t)b * a.bt_sb + (int64_t)lb * a.bt_sk] : -1;
+      const int id = slot_id;
       if (id >= 0 && id < a.num_blocks) {
         const int hg = tid / (D / 16);
         const int j = (tid - hg * (D / 16)) * 8;
