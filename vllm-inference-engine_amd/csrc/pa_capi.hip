@@ -174,12 +174,15 @@ static bool streamk_ok(int num_seqs, int num_kv_heads, int head_dim) {
 constexpr int kPairTilesMax = 128;
 // Tables of at most this many tiles keep one workgroup per pair, and a
 // stream-K range takes at least kSkMinRange tile positions (tiles plus segment
-// overhead). Measured on MI355X (14 q / 2 kv heads, head_dim 64, block 16,
-// equal lengths, caches evicted before each call): batch 1-32 x 2048 tokens
-// 33-35 us with one workgroup per pair, 18-21 us split with ranges of at least
-// 8 positions (16: 19-21 us, 64: 25-30 us); batch 4-32 x 128 tokens 13.7-14.2
-// us one per pair, 15.8-17 us split.
-constexpr int kPairShortTiles = 16;
+// overhead). Measured on MI355X with the current kernels (14 q / 2 kv heads,
+// head_dim 64, block 16, equal lengths, four pool copies rotated, rocprofv3
+// kernel durations), one workgroup per pair against stream-K ranges: batch
+// 1-32 x 512 tokens 6.5-8.1 us against 10.9-14.0 us; x 1024 tokens 8.3-11.3
+// us against 11.8-15.1 us; x 2048 tokens 14.9-17.2 us against 12.8-17.5 us
+// (batch 1-16 faster split). An earlier build with caches evicted: batch 1-32
+// x 2048 33-35 us one per pair, 18-21 us split with ranges of at least 8
+// positions (16: 19-21 us, 64: 25-30 us).
+constexpr int kPairShortTiles = 64;
 constexpr int kSkMinRange = 8;
 
 // Compute units of the current device (cached per device; threads that race
