@@ -39,6 +39,10 @@ sys.path.insert(0, str(REPO_ROOT / "vllm-inference-engine_amd"))
 
 HBM_PEAK_GBS = 8000.0
 TRAFFIC_SUMMARY = REPO_ROOT / "profiles" / "long_context_traffic.md"
+# GPU busy-wait (torch.cuda._sleep cycles, about 50 us on MI355X) enqueued before a timed call
+# whose kernel is shorter than the host's enqueue cost (about 19 us per call): the call is then
+# queued before the GPU reaches its start event, and the events bracket device time only.
+LEAD_CYCLES = 100_000
 
 
 def log(msg):
@@ -318,6 +322,9 @@ def attention_share_ms(dev, runner, seqs, iters=20):
         layer()
     torch.cuda.synchronize()
     a, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    # The GPU waits while the host queues every call, as in the decode step's graph replay:
+    # the events then time the calls' device work, not the host's enqueue cost.
+    torch.cuda._sleep(LEAD_CYCLES * iters)
     a.record()
     for _ in range(iters):
         layer()
@@ -512,8 +519,12 @@ def clone_workload(w):
                     unique_slots=w.unique_slots, meta=w.meta)
 
 
-def time_calls(copies, calls, warmup=5):
-    """HIP-event durations (ms) of `calls` attention calls rotating over the pool copies."""
+def time_calls(copies, calls, warmup=5, lead_cycles=0, host_us=None):
+    """HIP-event durations (ms) of `calls` attention calls rotating over the pool copies.
+
+    With `lead_cycles`, each call follows a GPU busy-wait outside its events. `host_us`, a
+    list, receives the host time of each call (enqueue only, nothing waits for the GPU).
+    """
     import torch
 
     from engine.kernels.paged_attention import paged_attention_decode_batched
@@ -529,15 +540,26 @@ def time_calls(copies, calls, warmup=5):
           for _ in range(calls)]
     for i, (a, b) in enumerate(ev):
         w = copies[i % len(copies)]
+        if lead_cycles:
+            torch.cuda._sleep(lead_cycles)
+        t0 = time.perf_counter()
         a.record()
         call(w)
         b.record()
+        if host_us is not None:
+            host_us.append((time.perf_counter() - t0) * 1e6)
     torch.cuda.synchronize()
     return [a.elapsed_time(b) for a, b in ev]
 
 
 def config_timings(dev, seed, copies=4, calls=50):
-    """The other measured shapes, each over rotated pool copies: mean and median of `calls`."""
+    """The other measured shapes, each over rotated pool copies: mean and median of `calls`.
+
+    `us_mean`/`us_median` are device time per call (each call follows a GPU busy-wait, so the
+    host's enqueue cost does not show in the events); `us_mean_back_to_back` times the same
+    calls issued back to back, where a kernel shorter than the host's enqueue cost is
+    host-bound; `host_enqueue_us_median` is the host's time per call.
+    """
     import torch
 
     from engine import workloads
@@ -551,7 +573,8 @@ def config_timings(dev, seed, copies=4, calls=50):
     for name, make in shapes:
         ws = [make()]
         ws += [clone_workload(ws[0]) for _ in range(copies - 1)]
-        ms = time_calls(ws, calls)
+        host = []
+        ms = time_calls(ws, calls, lead_cycles=LEAD_CYCLES, host_us=host)
         nbytes = ws[0].algorithmic_bytes(unique=True)
         mean, med = statistics.fmean(ms), statistics.median(ms)
         out[name] = {"num_seqs": ws[0].num_seqs, "num_q_heads": ws[0].q.shape[1],
@@ -560,7 +583,9 @@ def config_timings(dev, seed, copies=4, calls=50):
                      "us_mean": round(mean * 1e3, 2), "us_median": round(med * 1e3, 2),
                      "gbps": round(nbytes / (mean * 1e-3) / 1e9, 1),
                      "pct_of_hbm_peak": round(100 * nbytes / (mean * 1e-3) / 1e9 / HBM_PEAK_GBS, 2),
-                     "calls": calls, "pool_copies_rotated": copies}
+                     "calls": calls, "pool_copies_rotated": copies,
+                     "host_enqueue_us_median": round(statistics.median(host), 1),
+                     "us_mean_back_to_back": round(statistics.fmean(time_calls(ws, calls)) * 1e3, 2)}
         del ws
         torch.cuda.empty_cache()
     return out
