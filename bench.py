@@ -56,7 +56,8 @@ def parse_args():
     p.add_argument("--steps", type=int, default=50)
     p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--workload", default="long_context",
-                   help="long_context | gqa_sweep_kv{28,14,7,4} | qwen_layer | softmax_stress")
+                   help="long_context | gqa_sweep_kv{28,14,7,4} | qwen_layer | softmax_stress | "
+                        "decode_step_layer_b128")
     p.add_argument("--copies", type=int, default=4, help="rotated pool copies (cache defeat)")
     p.add_argument("--flush-mb", type=int, default=0,
                    help="write this many MB before each step's attention call (cache defeat "
@@ -344,6 +345,8 @@ def make_workload(name, device, seed):
         return workloads.qwen_layer(device=device, seed=seed)
     if name == "softmax_stress":
         return workloads.softmax_stress(device=device, seed=seed)
+    if name == "decode_step_layer_b128":
+        return workloads.decode_step_layer(128, device, seed)
     raise SystemExit(f"unknown workload {name}")
 
 
