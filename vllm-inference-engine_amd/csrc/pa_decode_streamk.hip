@@ -803,11 +803,24 @@ void decode_streamk_kernel(DecodeArgs a) {
     }
   };
 
-  // Arrivals this workgroup has counted and not yet resolved: thread t < npend
-  // counted one for pair s_mlist[t] and holds the value its counter increment
-  // returned.
+  // Arrivals this workgroup has listed and not yet resolved: thread t < npend
+  // listed one for pair s_mlist[t]; for t < ncounted it has also counted it
+  // and holds the value its counter increment returned.
   int npend = 0;
+  int ncounted = 0;
   int my_old = 0;
+
+  // Counts the listed arrivals not yet counted: every thread waits for its
+  // coherent record stores to complete, then each such arrival increments its
+  // pair's counter.
+  auto count_listed = [&]() {
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (tid >= ncounted && tid < npend)
+      my_old = __hip_atomic_fetch_add(a.cnt + s_mlist[tid], 1, __ATOMIC_RELAXED,
+                                      __HIP_MEMORY_SCOPE_AGENT);
+    ncounted = npend;
+  };
 
   // Resolves the counted arrivals: a pair whose count this workgroup completed
   // is merged here -- its records in a fixed order (suffix ranges, then prefix
@@ -816,6 +829,7 @@ void decode_streamk_kernel(DecodeArgs a) {
   // such pairs of the workgroup at once -- and its counter is reset to zero
   // for the next launch.
   auto resolve = [&]() {
+    count_listed();
     const int tid = wave * 64 + fresh_lane();
     const int my_pair = tid < npend ? s_mlist[tid] : 0;
     if (tid == 0) s_nmerge = 0;
@@ -910,22 +924,25 @@ void decode_streamk_kernel(DecodeArgs a) {
       __hip_atomic_store(a.cnt + s_mlist[e], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __syncthreads();
     npend = 0;
+    ncounted = 0;
   };
 
-  // Publishes a segment's records: every thread waits for its coherent stores
-  // to complete, then one arrival is counted for each of the n pairs pair_of(i)
-  // the records belong to. The returned counts are only needed when the
-  // workgroup resolves its arrivals, so the atomics' latency overlaps the rest
-  // of the range.
-  auto arrive = [&](int n, auto pair_of) {
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    if (tid >= npend && tid < npend + n) {
-      const int p = pair_of(tid - npend);
-      s_mlist[tid] = p;
-      my_old = __hip_atomic_fetch_add(a.cnt + p, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
+  // Lists a segment's arrival for each of the n pairs pair_of(i) its records
+  // belong to (thread npend + i holds pair i). A pair segment's arrival is
+  // counted later, when the workgroup next counts or resolves: its record
+  // stores then complete while the next segment streams, instead of holding
+  // up that segment's start. The returned counts are only needed when the
+  // workgroup resolves its arrivals.
+  auto list_arrival = [&](int n, auto pair_of) {
+    if (tid >= npend && tid < npend + n) s_mlist[tid] = pair_of(tid - npend);
     npend += n;
+  };
+  // Lists and counts at once (with every arrival listed before): a prefix
+  // item's records complete the counts of its group's members, whose pairs
+  // are spread over other workgroups and should merge as soon as they can.
+  auto arrive = [&](int n, auto pair_of) {
+    list_arrival(n, pair_of);
+    count_listed();
   };
 
   // Item containing list position x (in sequence b's items): kind (0 pair,
@@ -1052,7 +1069,7 @@ void decode_streamk_kernel(DecodeArgs a) {
       });
       if (!final_out) {
         const int p = b * NHG + idx;
-        arrive(1, [&](int) { return p; });
+        list_arrival(1, [&](int) { return p; });
       }
       __syncthreads();  // the merge state aliases the staging buffers of the next segment
     }
