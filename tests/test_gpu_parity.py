@@ -303,6 +303,26 @@ def test_merge_counters_return_to_zero(cuda_device):
     _check_workload(w, seqs=[0, 1, 7, 8, 31, 63])
 
 
+def test_calls_run_on_the_current_stream(cuda_device):
+    """The launch goes to the caller's current torch stream (a side stream here): the handle
+    the wrapper passes is that stream's, and the result equals the default stream's."""
+    from engine.kernels import _native
+
+    w = workloads.qwen_layer(device=cuda_device, seed=5)
+    want = paged_attention_decode_batched(w.q, w.k_cache, w.v_cache, w.block_tables,
+                                          w.seq_lens, w.scale)
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream(device=cuda_device)
+    with torch.cuda.stream(side):
+        assert _native.stream_handle(cuda_device) == side.cuda_stream
+        assert _native.stream_handle(torch.device("cuda")) == side.cuda_stream
+        got = paged_attention_decode_batched(w.q, w.k_cache, w.v_cache, w.block_tables,
+                                             w.seq_lens, w.scale)
+    side.synchronize()
+    assert _native.stream_handle(cuda_device) == torch.cuda.current_stream(cuda_device).cuda_stream
+    assert torch.equal(got, want)
+
+
 def test_paths_interleaved_on_one_stream(cuda_device):
     """Stream-K, fixed-split and two-pass calls alternate on one stream without
     disturbing each other's scratch: each result still matches the oracle."""

@@ -131,7 +131,16 @@ def ptr(t: torch.Tensor) -> int:
     return t.data_ptr()
 
 
+# torch's raw accessor of the current stream (what current_stream(d).cuda_stream
+# returns, without building a Stream object: about 0.2 us a call instead of 1.8).
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream_handle(device: torch.device) -> int:
+    """The HIP stream the caller's current torch stream on `device` wraps."""
+    if _raw_stream is not None:
+        idx = device.index if device.index is not None else torch.cuda.current_device()
+        return _raw_stream(idx)
     return torch.cuda.current_stream(device).cuda_stream
 
 
