@@ -218,11 +218,15 @@ static void streamk_plan(DecodeArgs& a, int num_seqs, int head_dim) {
   a.pair_per_wg = pairs <= want && tmax <= kPairTilesMax &&
                   (2 * pairs >= want || tmax <= kPairShortTiles);
   if (a.pair_per_wg) a.num_wg = pairs;
-  // A pair segment costs a workgroup about as long as streaming 240 KB of K/V
-  // (measured on MI355X: pipeline fill plus the drain and merge across
-  // wavefronts, 6-8 us per segment at the long-context shape).
+  // A pair segment costs a workgroup about as long as streaming 176 KB of K/V
+  // (pipeline fill, the drain and merge across wavefronts). Measured on MI355X
+  // (HIP events behind a GPU busy-wait, A/B on one box), budgets of 240, 208,
+  // 176 and 144 KB: long-context batch of 256 (lognormal ~4.6k tokens, shared
+  // prefixes) 101.1-101.6, 99.3-99.5, 99.0-99.1, 100.2-100.4 us; batch 64 x
+  // 2048 tokens at 7 kv heads, head_dim 128: 86.2, 85.3, 84.3-84.5, 84.2-84.3
+  // us; other shapes within 0.3 us.
   const int tile_bytes = 64 * a.head_group * head_dim;
-  a.seg_cost = (240 << 10) / tile_bytes;
+  a.seg_cost = (176 << 10) / tile_bytes;
   a.min_range = kSkMinRange;
   // Prefix items: only where ranges are used (one workgroup per pair cuts
   // nothing and merges nothing) and the kernel builds them.
