@@ -183,7 +183,12 @@ constexpr int kPairTilesMax = 128;
 // x 2048 33-35 us one per pair, 18-21 us split with ranges of at least 8
 // positions (16: 19-21 us, 64: 25-30 us).
 constexpr int kPairShortTiles = 64;
-constexpr int kSkMinRange = 8;
+// Ranges of at least 16 positions against 8, 32 and 64 (same shapes, HIP events
+// behind a GPU busy-wait, medians of 60 calls, one box): batch 1 x 2048 tokens
+// 14.8 against 15.4, 15.0 and 17.1 us; 4 x 2048 15.1 against 16.3, 15.2 and
+// 17.7; 1 x 4096 16.0 against 17.8, 16.2 and 17.1; 1 x 8192 18.7 against 23.2,
+// 17.8 and 18.9; batches that fill the GPU unchanged.
+constexpr int kSkMinRange = 16;
 
 // Compute units of the current device (cached per device; threads that race
 // on the first query store the same value).
