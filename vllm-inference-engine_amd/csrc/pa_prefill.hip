@@ -6,12 +6,13 @@
 // and sees pool rows 0 .. L - n + i.
 //
 // Work split. The (token, query head) pairs of one sequence and one kv head
-// form a list of n * g columns, token-major. A workgroup of four wavefronts
-// takes 128 consecutive columns (two groups of 16 per wavefront; 64 columns,
-// one group, at head_dim 256), so the K/V rows it stages serve all g query
-// heads of the kv head at once and each K or V operand read from LDS feeds
-// two MFMAs. Workgroups with the latest columns see the most keys; they are
-// numbered first so the longest runs start first.
+// form a list of n * g columns, token-major. A workgroup takes 128
+// consecutive columns (eight wavefronts of one group of 16 columns up to
+// head_dim 64, four wavefronts of two groups at head_dim 128, where each K or V
+// operand read from LDS feeds two MFMAs; 64 columns, one group per wavefront,
+// at head_dim 256), so the K/V rows it stages serve all g query heads of the
+// kv head at once. Workgroups with the latest columns see the most keys; they
+// are numbered first so the longest runs start first.
 //
 // Per key tile (128 keys up to head_dim 64, else 64) the workgroup loads K
 // and V rows (16-byte loads, block id per row from the table, fetched a tile
@@ -30,9 +31,8 @@ namespace pa {
 
 using namespace tiles;
 
-template <int D, int BS, int CG>
-__global__ __launch_bounds__(256) void prefill_attn_kernel(PrefillAttnArgs a) {
-  constexpr int NW = 4;
+template <int D, int BS, int CG, int NW>
+__global__ __launch_bounds__(64 * NW) void prefill_attn_kernel(PrefillAttnArgs a) {
   constexpr int COLS = 16 * CG * NW;  // columns per workgroup
   constexpr int KT = prefill_key_tile(D);  // keys per staged tile
   constexpr int NS = KT / 16;         // 16-key sub-tiles per tile
@@ -124,7 +124,7 @@ __global__ __launch_bounds__(256) void prefill_attn_kernel(PrefillAttnArgs a) {
   const int bs = BS > 0 ? BS : a.bs;
   u32x4 kr[PER], vr[PER];
   int ids[PER];
-  // Piece f = 256 i + tid of a tile is key row f / CPR, halves (f % CPR) * 8.
+  // Piece f = 64 NW i + tid of a tile is key row f / CPR, halves (f % CPR) * 8.
   // The block ids of a tile are loaded one tile before its K/V, so a K/V load
   // never waits on the table read it depends on.
   // Element strides fit 32 bits (the host checks it): a block's offset is one
@@ -435,13 +435,26 @@ __global__ __launch_bounds__(256) void prefill_attn_kernel(PrefillAttnArgs a) {
   if (tid == 0) __hip_atomic_store(a.cnt + blk, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// A column block of 64 CG columns runs as four wavefronts of CG groups of 16
+// columns; up to head_dim 64, a block of two groups per wavefront runs as
+// eight wavefronts of one group instead: the same columns and the same
+// arithmetic per column (the same result bits), four wavefronts per SIMD
+// instead of two (117 VGPRs instead of 218 at head_dim 64). Measured on MI355X
+// (HIP events, means of 30 calls, A/B on one box): one sequence of 8192 cached
+// + 1024 new tokens (split key ranges) 73.9-76.5 vs 78.8-78.9 us; 4 x (2048 +
+// 512) at head_dim 32 33.2-33.4 vs 33.9-34.1 us; 8 x (2048 + 512) at head_dim
+// 64 unchanged (68.7-69.7 vs 68.9). At head_dim 128 the eight-wavefront form
+// would hold one workgroup per CU (148 VGPRs), so four wavefronts stay.
 template <int D, int CG>
 static hipError_t launch_prefill_dc(const PrefillAttnArgs& a, hipStream_t s) {
   const int64_t grid = (int64_t)a.col_blocks * a.max_splits * a.num_seqs * a.hkv;
+  constexpr bool kEight = D <= 64 && CG == 2;
+  constexpr int CGK = kEight ? 1 : CG;
+  constexpr int NW = kEight ? 8 : 4;
   if (a.bs == 16)
-    hipLaunchKernelGGL((prefill_attn_kernel<D, 16, CG>), dim3((unsigned)grid), dim3(256), 0, s, a);
+    hipLaunchKernelGGL((prefill_attn_kernel<D, 16, CGK, NW>), dim3((unsigned)grid), dim3(64 * NW), 0, s, a);
   else
-    hipLaunchKernelGGL((prefill_attn_kernel<D, 0, CG>), dim3((unsigned)grid), dim3(256), 0, s, a);
+    hipLaunchKernelGGL((prefill_attn_kernel<D, 0, CGK, NW>), dim3((unsigned)grid), dim3(64 * NW), 0, s, a);
   return hipGetLastError();
 }
 
