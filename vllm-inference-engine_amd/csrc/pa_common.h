@@ -177,11 +177,12 @@ struct PrefillAttnArgs {
   float* recs;  // [seq][kv head][column block][split] records of (D + 2) x columns floats
 };
 
-// Column groups of 16 (token, query head) columns each prefill wavefront
-// takes (four wavefronts per workgroup): two below head_dim 256, where the
-// registers allow it, so each K and V operand read from LDS feeds two MFMAs.
-// Launches with few column blocks take one group instead (twice the
-// workgroups); see prefill_plan.
+// Columns of a prefill workgroup in units of 64 (token, query head) columns:
+// two (128 columns) below head_dim 256, where the registers allow it; the
+// kernel runs them as eight wavefronts of one group of 16 up to head_dim 64,
+// four wavefronts of two groups at head_dim 128 (each K and V operand read
+// from LDS then feeds two MFMAs). Launches with few column blocks take one
+// unit instead (twice the workgroups); see prefill_plan.
 __host__ __device__ constexpr int prefill_col_groups(int D) { return D <= 128 ? 2 : 1; }
 // The prefill workspace starts with a fixed region of arrival counters, one per
 // column block of a split launch, so that the counters of every launch sit at
