@@ -15,12 +15,15 @@ Output: one JSON line. value = bytes of one step (the attention call's
 algorithmic bytes: K/V at the distinct token slots read, Q, O, table entries,
 lengths; and the K/V write's rows, lengths and table entries) / mean step time,
 the K timed steps run back to back between two synchronisations with one HIP
-event pair on the launch stream around them. roofline.achieved = the attention
-call's algorithmic bytes / its mean duration over K calls enqueued back to back
-(one event pair around them). Beside them: per-call event timings (an event
-pair around each call adds a few microseconds of marker processing), the median
-of 60 such calls, the other measured shapes (one Qwen2.5-0.5B layer at batch 8, the GQA sweep, the softmax stress shape,
-one layer of the batch-128 decode step), the paged prefill attention against
+event pair on the launch stream around them (a GPU busy-wait before the start
+event lets the host queue the steps first, so the window holds device work
+only). roofline.achieved = the attention call's algorithmic bytes / its mean
+duration over K calls enqueued back to back (one event pair around them, the
+same busy-wait before it). Beside them: per-call event timings (an event pair
+around each call adds a few microseconds of marker processing), the median
+of 60 such calls, the other measured shapes (one Qwen2.5-0.5B layer at batch
+8, the GQA sweep, the softmax stress shape, one layer of the batch-128 decode
+step), the paged prefill attention against
 the MFMA peak, decode tokens/s of the Qwen2.5-0.5B-shaped model with and
 without fused decoder layers, and the reference's CPU algorithm timed on this
 host (the oracle's fp16 and fp32 attention over the headline batch, and two
@@ -527,6 +530,12 @@ def clone_workload(w):
                     unique_slots=w.unique_slots, meta=w.meta)
 
 
+def window_lead_cycles(n):
+    """GPU busy-wait (torch.cuda._sleep cycles) before a timed window of n calls: about 100 us
+    per call (at most 10 ms), more than the host needs to enqueue one."""
+    return 2 * LEAD_CYCLES * min(max(n, 1), 100)
+
+
 def window_calls(copies, calls, warmup=5):
     """Mean duration (ms) of `calls` attention calls enqueued back to back over the rotated
     pool copies, timed by one HIP event pair on the launch stream around all of them."""
@@ -542,6 +551,7 @@ def window_calls(copies, calls, warmup=5):
         call(copies[i % len(copies)])
     torch.cuda.synchronize()
     a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda._sleep(window_lead_cycles(calls))  # queue the calls before the GPU reaches them
     a.record()
     for i in range(calls):
         call(copies[i % len(copies)])
@@ -676,6 +686,10 @@ def main():
     # ~97 us kernel (rocprofv3 kernel durations against per-call events).
     t_start = torch.cuda.Event(enable_timing=True)
     t_end = torch.cuda.Event(enable_timing=True)
+    # A GPU busy-wait ahead of the start event lets the host queue the steps before the GPU
+    # reaches them: the window then holds the steps' device work and no host launch gaps (in
+    # a fresh process the host's first ~100 enqueues can fall behind a ~100 us step).
+    torch.cuda._sleep(window_lead_cycles(args.steps))
     t_start.record()
     for i in range(args.steps):
         step(args.warmup + i)
