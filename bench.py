@@ -464,7 +464,8 @@ def cpu_baseline(w, budget_s):
         "sample": (f"oracle literal fp16 path (per-sequence gather + einsum + softmax) over the "
                    f"whole headline batch ({w.num_seqs} sequences, {sum(w.lens)} tokens), "
                    f"{lit['passes']} whole pass(es) in {lit['seconds']} s; value counts the "
-                   "GPU value's bytes (shared prefix slots once) per whole pass"),
+                   "GPU attention call's algorithmic bytes (shared prefix slots once) per "
+                   "whole pass"),
         "fp16": lit,
         "fp32_upcast": out["fp32"],
     }
