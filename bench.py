@@ -106,7 +106,7 @@ def decode_benchmark(dev, model, prompts, steps, fuse_layers=True, attention_sha
     import torch
 
     from engine.kernels.paged_attention_integration import KernelPagedManualDecode
-    from engine.memory.block_pool import BlockTable
+    from engine.memory.block_allocator import BlockTable
     from types import SimpleNamespace
 
     batch = len(prompts)
@@ -406,6 +406,77 @@ def copy_ceiling(dev, nbytes=2 << 30, iters=10):
     return round(2 * nbytes / t / 1e9, 1)
 
 
+PROBE_LIB = REPO_ROOT / "vllm-inference-engine_amd" / "probes" / "libbw_probe_gfx950.so"
+
+
+def read_ceilings(dev, stream_bytes=1 << 30, pool_blocks=600_000, gather_blocks=150_000,
+                  block_bytes=4096, iters=20):
+    """Practical HBM read ceilings of this box, measured in the same run as the kernel.
+
+    read_stream_gbps: a 1 GiB buffer read once per launch with the decode kernel's load
+    instruction (16-byte non-temporal buffer loads, each wavefront instruction covering 1 KB,
+    16 KB in flight per wavefront). gather_4kb_gbps: 150,000 random 4 KB blocks of a 2.4 GB
+    pool (the headline pool's block size and about its distinct block count) read per launch,
+    four blocks in flight per wavefront, four disjoint block lists rotated so that no launch
+    finds the previous one's blocks in the 256 MB MALL. Both: the best of a few grid sizes,
+    `iters` launches back to back between one HIP event pair behind a GPU busy-wait.
+    """
+    import ctypes
+
+    import torch
+
+    lib = ctypes.CDLL(str(PROBE_LIB))
+    lib.bwp_read_stream.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p,
+                                    ctypes.c_int, ctypes.c_void_p]
+    lib.bwp_gather_blocks.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
+                                      ctypes.c_int, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p]
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    sink = torch.zeros(4, dtype=torch.int32, device=dev)
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+
+    def window(launch):
+        for _ in range(3):
+            launch(0)
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda._sleep(window_lead_cycles(iters))
+        a.record()
+        for i in range(iters):
+            launch(i)
+        b.record()
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) * 1e-3 / iters
+
+    out = {}
+    buf = torch.empty(stream_bytes, dtype=torch.uint8, device=dev).random_(0, 255)
+    nread = stream_bytes // (16 << 10) * (16 << 10)
+    best = 0.0
+    for grid in (cus, 2 * cus, 4 * cus):
+        def launch(i, grid=grid):
+            rc = lib.bwp_read_stream(buf.data_ptr(), stream_bytes, sink.data_ptr(), grid, stream)
+            assert rc == 0, f"bwp_read_stream failed ({rc})"
+        best = max(best, nread / window(launch) / 1e9)
+    out["read_stream_gbps"] = round(best, 1)
+    del buf
+    torch.cuda.empty_cache()
+    pool = torch.empty(pool_blocks * block_bytes, dtype=torch.uint8, device=dev).random_(0, 255)
+    gen = torch.Generator(device="cpu").manual_seed(123)
+    perm = torch.randperm(pool_blocks, generator=gen)[:4 * gather_blocks].to(torch.int32)
+    lists = perm.view(4, gather_blocks).to(dev)
+    best = 0.0
+    for grid in (cus, 2 * cus):
+        def launch(i, grid=grid):
+            rc = lib.bwp_gather_blocks(pool.data_ptr(), pool_blocks, block_bytes,
+                                       lists[i % 4].data_ptr(), gather_blocks, sink.data_ptr(),
+                                       grid, stream)
+            assert rc == 0, f"bwp_gather_blocks failed ({rc})"
+        best = max(best, gather_blocks * block_bytes / window(launch) / 1e9)
+    out["gather_4kb_gbps"] = round(best, 1)
+    del pool, lists
+    torch.cuda.empty_cache()
+    return out
+
+
 def cpu_attention_passes(w, budget_s, compute_dtype=None):
     """The oracle's attention (the reference's CPU PyTorch algorithm) over the workload's
     sequences, in whole passes over the batch until about budget_s of oracle time (or part of
@@ -595,12 +666,15 @@ def time_calls(copies, calls, warmup=5, lead_cycles=0, host_us=None):
 
 
 def config_timings(dev, seed, copies=4, calls=50):
-    """The other measured shapes, each over rotated pool copies: mean and median of `calls`.
+    """The other measured shapes, each over rotated pool copies.
 
-    `us_mean`/`us_median` are device time per call (each call follows a GPU busy-wait, so the
-    host's enqueue cost does not show in the events); `us_mean_back_to_back` times the same
-    calls issued back to back, where a kernel shorter than the host's enqueue cost is
-    host-bound; `host_enqueue_us_median` is the host's time per call.
+    `us_mean` (and gbps, pct_of_hbm_peak) is the headline's statistic: `calls` calls enqueued
+    back to back between one HIP event pair, behind a GPU busy-wait that lets the host queue
+    them first, so the window holds device time only. Beside it, per-call event pairs (each
+    call behind its own busy-wait; the pair adds a few microseconds of marker processing):
+    `us_mean_per_call_events`, `us_median_per_call_events`; the host's time per call
+    (`host_enqueue_us_median`), and the same calls issued back to back without the lead
+    (`us_mean_back_to_back`, host-bound where a kernel is shorter than the host's enqueue).
     """
     import torch
 
@@ -616,15 +690,18 @@ def config_timings(dev, seed, copies=4, calls=50):
         ws = [make()]
         ws += [clone_workload(ws[0]) for _ in range(copies - 1)]
         host = []
+        win = window_calls(ws, calls)
         ms = time_calls(ws, calls, lead_cycles=LEAD_CYCLES, host_us=host)
         nbytes = ws[0].algorithmic_bytes(unique=True)
         mean, med = statistics.fmean(ms), statistics.median(ms)
         out[name] = {"num_seqs": ws[0].num_seqs, "num_q_heads": ws[0].q.shape[1],
                      "num_kv_heads": ws[0].k_cache.shape[2], "head_dim": ws[0].k_cache.shape[3],
                      "total_tokens": sum(ws[0].lens), "algorithmic_bytes": nbytes,
-                     "us_mean": round(mean * 1e3, 2), "us_median": round(med * 1e3, 2),
-                     "gbps": round(nbytes / (mean * 1e-3) / 1e9, 1),
-                     "pct_of_hbm_peak": round(100 * nbytes / (mean * 1e-3) / 1e9 / HBM_PEAK_GBS, 2),
+                     "us_mean": round(win * 1e3, 2),
+                     "gbps": round(nbytes / (win * 1e-3) / 1e9, 1),
+                     "pct_of_hbm_peak": round(100 * nbytes / (win * 1e-3) / 1e9 / HBM_PEAK_GBS, 2),
+                     "us_mean_per_call_events": round(mean * 1e3, 2),
+                     "us_median_per_call_events": round(med * 1e3, 2),
                      "calls": calls, "pool_copies_rotated": copies,
                      "host_enqueue_us_median": round(statistics.median(host), 1),
                      "us_mean_back_to_back": round(statistics.fmean(time_calls(ws, calls)) * 1e3, 2)}
@@ -781,6 +858,12 @@ def main():
         f"{attn_window_ms * 1e3:.1f} us per call back to back ({achieved:.0f} GB/s), "
         f"{attn_mean * 1e3:.1f} us between per-call events")
     result["copy_ceiling_gbps"] = copy_ceiling(dev)
+    ceil = read_ceilings(dev)
+    result["read_ceiling_gbps"] = ceil["read_stream_gbps"]
+    result["gather_ceiling_gbps"] = ceil["gather_4kb_gbps"]
+    result["roofline"]["frac_of_gather_ceiling"] = round(achieved / ceil["gather_4kb_gbps"], 4)
+    log(f"ceilings: copy {result['copy_ceiling_gbps']} GB/s, read {ceil['read_stream_gbps']} "
+        f"GB/s, 4 KB gather {ceil['gather_4kb_gbps']} GB/s")
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(base, args.cpu_seconds)
         log(f"cpu baseline: {result['cpu_baseline']['value']} GB/s")

@@ -194,3 +194,48 @@ def test_noalloc_entry_refuses_what_its_scratch_cannot_hold():
     assert lib.pa_decode_batched_noalloc_f16(*args, 4, 14, 2, 48, 16, 100, 64, 0.125, None) == \
         _native.PA_ERR_UNSUPPORTED  # head_dim outside the built set, as for the workspace entry
 
+
+
+def test_rope_decode_refuses_an_empty_table_before_launch():
+    """The fused RoPE + K/V write + attention entry checks the table width and the
+    output strides on the host, as pa_decode_batched_f16 does, for both of its forms."""
+    lib = _native.load()
+    rows = _strides(896, 64, 1)
+    kv_rows = _strides(128, 64, 1)
+    cs = _strides(64, 1)
+    pool = _strides(2048, 128, 64, 1)
+
+    def call(max_blocks, out_str=(896, 64, 1)):
+        return lib.pa_decode_rope_batched_f16(
+            16, rows, 16, kv_rows, 16, kv_rows, 16, cs, 16, cs, 16, pool, 16, pool,
+            16, _strides(max(max_blocks, 1), 1), 16, 16, _strides(*out_str),
+            4, 14, 2, 64, 16, 100, max_blocks, 0.125, 16, 1 << 30, None)
+
+    assert call(0) == _native.PA_ERR_ARG
+    assert b"at least one column" in lib.pa_last_error()
+    assert call(-3) == _native.PA_ERR_ARG
+    assert call(4, out_str=(896, 64, 2)) == _native.PA_ERR_ARG
+    assert b"out" in lib.pa_last_error()
+
+
+def test_bandwidth_probe_library_exports_its_header():
+    """The benchmark's read-ceiling probes (include/bw_probe.h) load and check their
+    arguments on the host before any launch."""
+    import ctypes
+
+    hdr = HEADER.with_name("bw_probe.h").read_text()
+    names = sorted(set(re.findall(r"BWP_API\s+int\s+(bwp_\w+)\s*\(", hdr)))
+    assert names == ["bwp_gather_blocks", "bwp_read_stream"]
+    lib = ctypes.CDLL(str(Path(_native.__file__).resolve().parents[2] / "probes" /
+                          "libbw_probe_gfx950.so"))
+    for n in names:
+        assert hasattr(lib, n)
+    lib.bwp_read_stream.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p,
+                                    ctypes.c_int, ctypes.c_void_p]
+    lib.bwp_gather_blocks.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
+                                      ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p,
+                                      ctypes.c_int, ctypes.c_void_p]
+    assert lib.bwp_read_stream(None, 1 << 20, 16, 256, None) == 1
+    assert lib.bwp_read_stream(24, 1 << 20, 16, 256, None) == 1  # misaligned buffer
+    assert lib.bwp_gather_blocks(16, 100, 8192, 16, 10, 16, 256, None) == 1  # block > 4 KB
+    assert lib.bwp_gather_blocks(16, 100, 1000, 16, 10, 16, 256, None) == 1  # not whole KB

@@ -65,7 +65,7 @@ def paged_greedy(runner, prompts, steps, forced=None, keep=None):
 
     Returns every sequence's tokens and the per-step logits (fp32, cpu) of the
     sequences in `keep` (all of them when None; the others get None)."""
-    from engine.memory.block_pool import BlockTable
+    from engine.memory.block_allocator import BlockTable
 
     bs = runner.block_size
     alloc = runner.allocator
@@ -242,7 +242,7 @@ def test_single_sequence_generate_matches_batched_path(cuda_device):
 def test_shared_write_block_is_refused(cuda_device):
     """A decode write into a block with ref_count > 1 raises (reference integration.py:587-592)."""
     from engine.kernels.paged_attention_integration import KernelPagedManualDecode
-    from engine.memory.block_pool import BlockTable
+    from engine.memory.block_allocator import BlockTable
 
     model = make_model(TINY, 4, cuda_device)
     runner = KernelPagedManualDecode(model, block_size=16, num_blocks=8, device=str(cuda_device))
@@ -264,7 +264,7 @@ def _twin_runners(model, device, prompts, bs=16, num_blocks=256, max_graphs=32):
 
 
 def _prefilled(runner, i, prompt):
-    from engine.memory.block_pool import BlockTable
+    from engine.memory.block_allocator import BlockTable
 
     bs = runner.block_size
     bt = BlockTable(i, bs, [runner.allocator.allocate() for _ in range((len(prompt) + bs - 1) // bs)],

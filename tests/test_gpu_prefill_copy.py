@@ -108,7 +108,7 @@ def test_prefill_keeps_hit_blocks_and_copies_only_owned_blocks(cuda_device, capl
     log line reports no difference (:91)."""
     import logging
 
-    from engine.memory.block_pool import BlockTable
+    from engine.memory.block_allocator import BlockTable
 
     caplog.set_level(logging.INFO, logger="engine.kernels.paged_attention_integration")
     runner = _runner(FakePrefillModel(cuda_device), "share", cuda_device, debug=True)
@@ -137,7 +137,7 @@ def test_debug_prefix_cache_reports_the_largest_difference(cuda_device, caplog):
     reference's per-token loop (integration.py:328-362) restated as one device reduction."""
     import logging
 
-    from engine.memory.block_pool import BlockTable
+    from engine.memory.block_allocator import BlockTable
 
     caplog.set_level(logging.INFO, logger="engine.kernels.paged_attention_integration")
     runner = _runner(FakePrefillModel(cuda_device), "share", cuda_device, debug=True)
@@ -157,7 +157,7 @@ def test_debug_prefix_cache_reports_the_largest_difference(cuda_device, caplog):
 
 def test_full_prefill_uses_cached_prefix_and_only_forwards_suffix(cuda_device):
     """Reference fixture :94-125: "full" mode forwards only the suffix over the cached prefix."""
-    from engine.memory.block_pool import BlockTable
+    from engine.memory.block_allocator import BlockTable
 
     model = FakePrefillModel(cuda_device)
     runner = _runner(model, "full", cuda_device)
@@ -180,7 +180,7 @@ def test_full_prefill_uses_cached_prefix_and_only_forwards_suffix(cuda_device):
 
 def test_full_prefill_with_zero_hit_uses_normal_full_prompt_path(cuda_device):
     """Reference fixture :129-151: no cached tokens in "full" mode forwards the whole prompt."""
-    from engine.memory.block_pool import BlockTable
+    from engine.memory.block_allocator import BlockTable
 
     model = FakePrefillModel(cuda_device)
     runner = _runner(model, "full", cuda_device)
@@ -195,7 +195,7 @@ def test_full_prefill_with_zero_hit_uses_normal_full_prompt_path(cuda_device):
 
 def test_full_prefill_handles_cached_prefix_and_single_remaining_token(cuda_device):
     """Reference fixture :154-182: one block cached, one prompt token left to forward."""
-    from engine.memory.block_pool import BlockTable
+    from engine.memory.block_allocator import BlockTable
 
     model = FakePrefillModel(cuda_device)
     runner = _runner(model, "full", cuda_device)

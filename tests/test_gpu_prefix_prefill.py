@@ -50,7 +50,7 @@ def make_runner(model, device, paged_prefill):
 
 
 def seq(seq_id, tokens, ids, cached):
-    from engine.memory.block_pool import BlockTable
+    from engine.memory.block_allocator import BlockTable
 
     bt = BlockTable(seq_id=seq_id, block_size=16, physical_block_ids=list(ids),
                     num_tokens=len(tokens))

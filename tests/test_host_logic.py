@@ -78,7 +78,7 @@ def _cpu_runner():
 
 def test_runner_refuses_writes_without_a_block_or_into_shared_blocks():
     """Host-side guards of decode_step (reference integration.py:580-592) run before any kernel."""
-    from engine.memory.block_pool import BlockTable
+    from engine.memory.block_allocator import BlockTable
 
     runner = _cpu_runner()
     full = BlockTable(0, 16, [runner.allocator.allocate()], 16)  # block full, no next block
@@ -97,9 +97,9 @@ def test_runner_refuses_writes_without_a_block_or_into_shared_blocks():
 
 
 def test_free_list_allocator_counts_references():
-    from engine.memory.block_pool import BlockTable, FreeListAllocator
+    from engine.memory.block_allocator import BlockTable, BlockAllocator
 
-    a = FreeListAllocator(3)
+    a = BlockAllocator(3)
     ids = [a.allocate() for _ in range(3)]
     assert not a.can_allocate(1)
     with pytest.raises(MemoryError):
@@ -108,7 +108,7 @@ def test_free_list_allocator_counts_references():
     t = BlockTable(0, 16, list(ids), 40)
     assert t.num_blocks_needed_for(40) == 3 and t.last_block_has_space()
     t.free(a)
-    assert a.num_free == 2 and a.ref_counts == {ids[0]: 1}
+    assert a.num_free_blocks == 2 and a.ref_counts == {ids[0]: 1}
     with pytest.raises(ValueError):
         a.free(ids[1])
 

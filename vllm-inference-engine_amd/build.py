@@ -1,8 +1,9 @@
 """Build recipe for the gfx950 paged-attention library.
 
 Compiles every HIP source under csrc/ with hipcc for gfx950 and links them into
-engine/kernels/libpa_gfx950.so, next to the ctypes loader that opens it. Object
-files go to _build/ at the repository root. Run directly
+engine/kernels/libpa_gfx950.so, next to the ctypes loader that opens it, and the
+benchmark's read-bandwidth probes (probes/bw_probe.hip) into
+probes/libbw_probe_gfx950.so. Object files go to _build/ at the repository root. Run directly
 (``python vllm-inference-engine_amd/build.py``) or through
 ``__graft_entry__.build()``.
 """
@@ -21,6 +22,8 @@ CSRC = PKG_DIR / "csrc"
 INCLUDE = REPO_ROOT / "include"
 BUILD_DIR = REPO_ROOT / "_build"
 LIB_PATH = PKG_DIR / "engine" / "kernels" / "libpa_gfx950.so"
+PROBE_SRC = PKG_DIR / "probes" / "bw_probe.hip"
+PROBE_LIB = PKG_DIR / "probes" / "libbw_probe_gfx950.so"
 
 ARCH = "gfx950"
 
@@ -71,23 +74,28 @@ def _compile_one(src: Path) -> Path:
     return obj
 
 
-def build(verbose: bool = False) -> Path:
-    """Compile all sources and link the shared library; returns its path."""
-    BUILD_DIR.mkdir(parents=True, exist_ok=True)
-    srcs = _sources()
-    if not srcs:
-        raise RuntimeError(f"no HIP sources under {CSRC}")
-    with concurrent.futures.ThreadPoolExecutor(max_workers=min(8, len(srcs))) as ex:
-        objs = list(ex.map(_compile_one, srcs))
-    tmp = LIB_PATH.with_suffix(".so.tmp")
+def _link(objs: list[Path], lib: Path) -> None:
+    tmp = lib.with_suffix(".so.tmp")
     cmd = [_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs),
            "-Wl,-rpath,/opt/rocm/lib", "-o", str(tmp)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
-        raise RuntimeError(f"link failed:\n{proc.stdout}\n{proc.stderr}")
-    os.replace(tmp, LIB_PATH)
+        raise RuntimeError(f"link of {lib.name} failed:\n{proc.stdout}\n{proc.stderr}")
+    os.replace(tmp, lib)
+
+
+def build(verbose: bool = False) -> Path:
+    """Compile all sources and link the shared libraries; returns the attention library's path."""
+    BUILD_DIR.mkdir(parents=True, exist_ok=True)
+    srcs = _sources()
+    if not srcs:
+        raise RuntimeError(f"no HIP sources under {CSRC}")
+    with concurrent.futures.ThreadPoolExecutor(max_workers=min(8, len(srcs) + 1)) as ex:
+        objs = list(ex.map(_compile_one, srcs + [PROBE_SRC]))
+    _link(objs[:-1], LIB_PATH)
+    _link(objs[-1:], PROBE_LIB)
     if verbose:
-        print(f"built {LIB_PATH} from {len(srcs)} sources", file=sys.stderr)
+        print(f"built {LIB_PATH} from {len(srcs)} sources and {PROBE_LIB}", file=sys.stderr)
     return LIB_PATH
 
 

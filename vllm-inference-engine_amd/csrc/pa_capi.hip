@@ -846,6 +846,21 @@ int pa_decode_rope_batched_f16(const void* q, const int64_t q_strides[3], const 
   int rc = check_common(q, k_cache, v_cache, out, k_strides, v_strides, num_q_heads, num_kv_heads,
                         head_dim, block_size, num_blocks);
   if (rc) return rc;
+  // What pa_decode_batched_f16 requires of the table and the output holds for
+  // both forms (q may have any strides: the two-launch form rotates it into a
+  // contiguous copy, and the one-launch form is taken only for aligned rows).
+  if (max_blocks_per_seq <= 0) {
+    set_error("block table needs at least one column");
+    return PA_ERR_ARG;
+  }
+  if (out_strides[2] != 1 || out_strides[0] % 4 || out_strides[1] % 4) {
+    set_error("out needs unit head_dim stride and 4-element aligned strides");
+    return PA_ERR_ARG;
+  }
+  if (num_seqs > 65535) {
+    set_error("num_seqs %d exceeds the grid limit 65535", num_seqs);
+    return PA_ERR_UNSUPPORTED;
+  }
   const size_t ws_need = pa_decode_rope_batched_workspace_bytes(
       num_seqs, num_q_heads, num_kv_heads, head_dim, block_size, max_blocks_per_seq);
   if (!workspace || workspace_bytes < ws_need) {

@@ -35,12 +35,13 @@ import numpy as np
 import torch
 import torch.nn as nn
 
-from . import _native
-from .paged_attention import (
+from engine.kernels import _native
+from engine.kernels.paged_attention import (
     _on_device,
     pad_block_tables,
     paged_attention_prefill,
 )
+from engine.memory.block_allocator import BlockAllocator, BlockTable, PhysicalBlockPool
 
 logger = logging.getLogger(__name__)
 
@@ -252,6 +253,7 @@ def paged_rope_decode_attention(
     out = torch.empty((num_seqs, num_q_heads, head_dim), dtype=torch.float16, device=query.device)
     if num_seqs == 0:
         return out
+    assert block_tables.shape[1] > 0, "block_tables needs at least one column"
     lib = _native.load()
     dev = query.device
     max_blocks = block_tables.shape[1]
@@ -890,8 +892,6 @@ class KernelPagedManualDecode:
         fuse_layers: bool = True,
         max_graphs: int = 32,
     ):
-        from ..memory.block_pool import FreeListAllocator, PhysicalBlockPool
-
         if prefix_mode not in ("off", "share", "full"):
             raise ValueError(f"Unsupported prefix_mode {prefix_mode!r}; expected 'off', 'share', or 'full'.")
         self.model = model
@@ -907,15 +907,14 @@ class KernelPagedManualDecode:
         self.head_dim = getattr(config, "head_dim", None) or (
             config.hidden_size // config.num_attention_heads)
         if num_blocks is None:
-            free, _ = torch.cuda.mem_get_info(self.device)
-            per_block = (2 * self.num_layers * block_size * self.num_kv_heads * self.head_dim
-                         * torch.tensor([], dtype=dtype).element_size())
-            num_blocks = max(1, int(free * gpu_memory_utilization) // per_block)
+            from engine.memory.block_allocator import compute_num_blocks
+            num_blocks = max(1, compute_num_blocks(config, block_size, gpu_memory_utilization,
+                                                   self.device, dtype))
         self.num_blocks = num_blocks
         self.pool = PhysicalBlockPool(num_blocks=num_blocks, block_size=block_size,
                                       num_layers=self.num_layers, num_kv_heads=self.num_kv_heads,
                                       head_dim=self.head_dim, dtype=dtype, device=self.device)
-        self.allocator = FreeListAllocator(num_blocks)
+        self.allocator = BlockAllocator(num_blocks=num_blocks)
         self._grad_probed = False
         # Batched decode steps replay captured HIP graphs, one per (batch-size
         # bucket, table width rounded up to a multiple of 64 blocks), at most
@@ -1150,8 +1149,6 @@ class KernelPagedManualDecode:
 
         `prompt` is a string (needs a tokenizer) or a list of token ids.
         """
-        from ..memory.block_pool import BlockTable
-
         alloc = allocator or self.allocator
         if isinstance(prompt, str):
             input_ids = self.tokenizer(prompt, return_tensors="pt").input_ids.to(self.device)
