@@ -54,11 +54,27 @@ enum {
  * 7: residual input of pa_rmsnorm_f16, pa_top2_f16; 8: pa_linear_f16; 9: pa_linear_f16
  * removed, decode workspace sizes stated per current device; 10:
  * pa_decode_batched_noalloc_f16; 11: pa_decode_rope_batched_f16, decode workspace
- * with room for shared-prefix records). */
+ * with room for shared-prefix records; 12: pa_decode_batched_schedule). */
 PA_API int pa_abi_version(void);
 
 /* Message of the last failed call on this thread ("" after a success). */
 PA_API const char* pa_last_error(void);
+
+/*
+ * The schedule pa_decode_batched_f16 picks for these sizes on the current
+ * device, for a contiguous pool [num_blocks, block_size, num_kv_heads,
+ * head_dim]; host only, no launch. No counterpart in the reference (its
+ * Triton launch picks a tile size only, paged_attention.py:665-673); for
+ * tests and tools that need to know which kernel path a shape takes.
+ * info[0]: 0 stream-K ranges (decode_streamk_kernel), 1 one workgroup per
+ * (sequence, kv-head group) pair (decode_pair_kernel), 2 fixed 512-token
+ * splits (more than 1024 sequences); info[1]: kv heads per pair; info[2]:
+ * workgroups of the launch; info[3]: 1 when the launch looks for shared
+ * prefixes (prefix items), else 0.
+ */
+PA_API int pa_decode_batched_schedule(int num_seqs, int num_q_heads, int num_kv_heads,
+                                      int head_dim, int block_size, int max_blocks_per_seq,
+                                      int info[4]);
 
 /*
  * Batched GQA paged decode attention, online softmax with split-K partitions.
@@ -315,10 +331,16 @@ PA_API int pa_top2_f16(const void* logits, int64_t row_stride, int rows, int voc
  * harnesses that forbid allocation. Same arguments, kernels and results (the
  * same bits) as pa_decode_batched_f16, without the workspace: the split-K
  * scratch lives in a fixed array of PA_NOALLOC_SCRATCH_BYTES that the library
- * holds on each GPU it runs on until the process ends. Calls whose scratch
- * need exceeds it, and batches beyond the stream-K plan (more than 1024
- * sequences or 65536 sequence x kv-head-group pairs), are refused with
- * PA_ERR_UNSUPPORTED before any launch. Every call on one GPU uses that GPU's
+ * holds on each GPU it runs on until the process ends. One exception: where
+ * the shared-prefix records of a stream-K launch would not fit the array
+ * (head_dim 64: from 466 sequences at 2 kv heads, 117 at 8; in general
+ * 262144 + 2 x 256 x 4 x R + 2 x num_seqs x num_kv_heads x R > 16 MiB with R =
+ * (32 + 16 x head_dim) x 4 bytes), the call reads shared prefixes once per
+ * sequence instead: results within the attention tolerance of
+ * pa_decode_batched_f16 but not the same bits (the sums run in another order).
+ * Calls whose scratch need still exceeds the array, and batches beyond the
+ * stream-K plan (more than 1024 sequences or 65536 sequence x kv-head-group
+ * pairs), are refused with PA_ERR_UNSUPPORTED before any launch. Every call on one GPU uses that GPU's
  * one array: calls that overlap in time on one GPU (concurrent streams or
  * threads) race and must not be made; calls ordered on one stream are fine.
  * The first call on a device also launches a small fill kernel, on the call's

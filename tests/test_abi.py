@@ -239,3 +239,24 @@ def test_bandwidth_probe_library_exports_its_header():
     assert lib.bwp_read_stream(24, 1 << 20, 16, 256, None) == 1  # misaligned buffer
     assert lib.bwp_gather_blocks(16, 100, 8192, 16, 10, 16, 256, None) == 1  # block > 4 KB
     assert lib.bwp_gather_blocks(16, 100, 1000, 16, 10, 16, 256, None) == 1  # not whole KB
+
+
+def test_schedule_query_names_each_path():
+    """pa_decode_batched_schedule reports the path a shape takes, with no launch (the CU
+    count is the current device's, 256 without a GPU as on an MI355X)."""
+    cus = _device_cus()
+    # One Qwen2.5-0.5B layer at batch 8: 16 short pairs, one workgroup each, no sharing.
+    s = _native.decode_schedule(8, 14, 2, 64, 16, 32)
+    assert s == {"path": "pair_per_workgroup", "kv_heads_per_pair": 1, "workgroups": 16,
+                 "shared_prefixes": False}
+    # Batch 256 of long sequences: stream-K ranges, two kv heads per pair, one workgroup per
+    # CU, prefix sharing searched.
+    s = _native.decode_schedule(256, 14, 2, 64, 16, 2048)
+    assert s == {"path": "stream_k", "kv_heads_per_pair": 2 if 512 > cus else 1,
+                 "workgroups": cus, "shared_prefixes": True}
+    # Block size 8 never shares; more than 1024 sequences take the fixed splits.
+    assert not _native.decode_schedule(256, 14, 2, 64, 8, 4096)["shared_prefixes"]
+    assert _native.decode_schedule(1100, 14, 2, 64, 16, 64)["path"] == "fixed_split"
+    lib = _native.load()
+    info = (ctypes.c_int * 4)()
+    assert lib.pa_decode_batched_schedule(8, 14, 2, 48, 16, 32, info) == _native.PA_ERR_ARG

@@ -274,10 +274,10 @@ def test_large_batch_fixed_split_path(cuda_device, d):
                                          w.scale)
     torch.cuda.synchronize()
     assert torch.count_nonzero(out[0]) == 0
-    seqs = [1, 2, 3, 500, 1099] + [int(i) for i in np.argsort(lens)[-3:]]
+    seqs = list(range(1, len(lens)))  # every row (row 0 is empty and checked above)
     q, k, v, tables, ls = workloads.gather_subset(w, seqs)
     err = max_err(out[seqs], oracle32(q, k, v, tables, ls, w.scale))
-    print(f"[parity] fixed-split path D{d}: max abs err {err:.3e}", flush=True)
+    print(f"[parity] fixed-split path D{d}: {len(seqs)} rows, max abs err {err:.3e}", flush=True)
     assert err <= TOL
 
 

@@ -135,6 +135,16 @@ def test_query_group_sizes(cuda_device, hkv, g):
 
 
 def test_short_shares_are_read_per_sequence(cuda_device):
-    # Pairs sharing two blocks: too little to pay for a prefix item; any mix must agree.
-    spec = [(400, 0), (300, 2), (500, 0), (600, 1), (800, 0), (700, 40)]
-    check(build(spec, 2, 7, 64, 16, 17, cuda_device), "short shares")
+    # Sequences sharing 1, 2 or 40 blocks with their predecessor: too little to pay for a
+    # prefix item (the reads saved must outweigh the item's fixed cost), so each is read per
+    # sequence; beside them a run of three sharing 64 blocks, which does get a prefix item.
+    # Lengths above 128 tiles keep the launch on the stream-K kernel that builds prefix
+    # items (shorter tables would take one workgroup per pair, which never shares).
+    from engine.kernels import _native
+
+    spec = [(2400, 0), (2300, 2), (2500, 0), (2600, 1), (2800, 0), (2700, 40),
+            (3000, 0), (2900, 64), (2200, 64)]
+    case = build(spec, 2, 7, 64, 16, 17, cuda_device)
+    sched = _native.decode_schedule(len(case["lens"]), 14, 2, 64, 16, case["bt"].shape[1])
+    assert sched["path"] == "stream_k" and sched["shared_prefixes"], sched
+    check(case, "short shares")

@@ -324,7 +324,7 @@ using namespace pa;
 
 extern "C" {
 
-int pa_abi_version(void) { return 11; }
+int pa_abi_version(void) { return 12; }
 
 const char* pa_last_error(void) { return g_error.c_str(); }
 
@@ -342,6 +342,38 @@ size_t pa_decode_batched_workspace_bytes(int num_seqs, int num_q_heads, int num_
   const int64_t ms = splits_for(max_tiles_for(max_blocks_per_seq, block_size), st);
   if (ms <= 1) return 0;
   return kSkCounterBytes + (size_t)num_seqs * num_kv_heads * ms * record_floats(head_dim) * sizeof(float);
+}
+
+int pa_decode_batched_schedule(int num_seqs, int num_q_heads, int num_kv_heads, int head_dim,
+                               int block_size, int max_blocks_per_seq, int info[4]) {
+  clear_error();
+  if (!info || num_seqs <= 0 || num_q_heads <= 0 || num_kv_heads <= 0 ||
+      num_q_heads % num_kv_heads || num_q_heads / num_kv_heads > 16 || block_size <= 0 ||
+      max_blocks_per_seq <= 0 || !supported_head_dim(head_dim)) {
+    set_error("invalid or unsupported sizes");
+    return PA_ERR_ARG;
+  }
+  if (!streamk_ok(num_seqs, num_kv_heads, head_dim)) {
+    info[0] = 2;
+    info[1] = 1;
+    info[2] = num_seqs;
+    info[3] = 0;
+    return PA_OK;
+  }
+  DecodeArgs a{};
+  a.hkv = num_kv_heads;
+  a.g = num_q_heads / num_kv_heads;
+  a.bs = block_size;
+  a.max_blocks = max_blocks_per_seq;
+  // A contiguous pool [num_blocks, block_size, num_kv_heads, head_dim].
+  a.k_st = a.v_st = (int64_t)num_kv_heads * head_dim;
+  a.k_sh = a.v_sh = head_dim;
+  streamk_plan(a, num_seqs, head_dim);
+  info[0] = a.pair_per_wg ? 1 : 0;
+  info[1] = a.head_group;
+  info[2] = a.num_wg;
+  info[3] = a.share;
+  return PA_OK;
 }
 
 int pa_decode_batched_f16(const void* q, const int64_t q_strides[3], const void* k_cache,

@@ -17,7 +17,7 @@ import torch  # noqa: F401  (must be loaded before the HIP library, see above)
 
 LIB_NAME = "libpa_gfx950.so"
 LIB_PATH = Path(__file__).with_name(LIB_NAME)
-ABI_VERSION = 11
+ABI_VERSION = 12
 
 PA_OK = 0
 PA_ERR_ARG = 1
@@ -40,6 +40,8 @@ SIGNATURES: dict[str, tuple] = {
         _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _vp, _i64p,
         _i32, _i32, _i32, _i32, _i32, _i32, _i32, _f32, _vp, _sz, _vp]),
     "pa_decode_batched_workspace_bytes": (_sz, [_i32, _i32, _i32, _i32, _i32, _i32]),
+    "pa_decode_batched_schedule": (_i32, [_i32, _i32, _i32, _i32, _i32, _i32,
+                                          ctypes.POINTER(ctypes.c_int)]),
     "pa_decode_v2_f16": (_i32, [
         _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64, _i32, _i32, _vp, _i64p,
         _i32, _i32, _i32, _i32, _i32, _f32, _vp, _sz, _vp]),
@@ -212,3 +214,15 @@ def check(status: int, what: str) -> None:
     if status != PA_OK:
         msg = load().pa_last_error().decode(errors="replace")
         raise NativeLibraryError(f"{what} failed (status {status}): {msg}")
+
+
+def decode_schedule(num_seqs: int, num_q_heads: int, num_kv_heads: int, head_dim: int,
+                    block_size: int, max_blocks: int) -> dict:
+    """The kernel path pa_decode_batched_f16 takes for these sizes (host only, no launch)."""
+    info = (ctypes.c_int * 4)()
+    check(load().pa_decode_batched_schedule(num_seqs, num_q_heads, num_kv_heads, head_dim,
+                                            block_size, max_blocks, info),
+          "pa_decode_batched_schedule")
+    path = {0: "stream_k", 1: "pair_per_workgroup", 2: "fixed_split"}[info[0]]
+    return {"path": path, "kv_heads_per_pair": info[1], "workgroups": info[2],
+            "shared_prefixes": bool(info[3])}

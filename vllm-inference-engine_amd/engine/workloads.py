@@ -107,6 +107,19 @@ def make_random(num_seqs, num_q_heads, num_kv_heads, head_dim, lens, block_size=
     return _finish(name, q, k, v, tables, lens, head_dim ** -0.5, sum(lens), device)
 
 
+def from_tables(tables, lens, num_q_heads, num_kv_heads, head_dim, block_size, num_blocks,
+                seed=0, device="cpu", name="tables") -> Workload:
+    """Workload over given block tables (which may repeat blocks across sequences, as a
+    prefix cache's shared prompts do): N(0, 1) q and pool, distinct slots counted once."""
+    gen = torch.Generator(device=device).manual_seed(seed)
+    q = _randn((len(tables), num_q_heads, head_dim), gen, device)
+    shape = (num_blocks, block_size, num_kv_heads, head_dim)
+    k = _randn(shape, gen, device)
+    v = _randn(shape, gen, device)
+    slots = {(t[i // block_size], i % block_size) for t, n in zip(tables, lens) for i in range(n)}
+    return _finish(name, q, k, v, tables, lens, head_dim ** -0.5, len(slots), device)
+
+
 def qwen_layer(device="cpu", seed=0) -> Workload:
     rng = np.random.default_rng(seed)
     lens = rng.integers(1, 513, size=8).tolist()
