@@ -87,6 +87,13 @@ def parse_args():
                    help="skip the decode-step tokens/sec measurement")
     p.add_argument("--no-prefill", action="store_true",
                    help="skip the prefix-prefill attention measurement")
+    p.add_argument("--profile-workloads", default="",
+                   help="comma-separated workloads: run --profile-calls attention calls of each "
+                        "(4 rotated pool copies) and exit, for rocprofv3 kernel statistics")
+    p.add_argument("--profile-calls", type=int, default=40)
+    p.add_argument("--library", default="",
+                   help="file name of another build of the library in engine/kernels/ to load "
+                        "instead of libpa_gfx950.so (A/B profiles)")
     p.add_argument("--decode-batch", type=int, default=128)
     p.add_argument("--decode-steps", type=int, default=128)
     return p.parse_args()
@@ -723,6 +730,22 @@ def main():
     from engine.kernels.paged_attention_integration import paged_kv_write
 
     dev = torch.device("cuda", 0)
+    if args.library:
+        from engine.kernels import _native
+        _native.LIB_PATH = _native.LIB_PATH.with_name(args.library)
+    if args.profile_workloads:
+        for name in args.profile_workloads.split(","):
+            base = make_workload(name, dev, args.seed)
+            ws = [base] + [clone_workload(base) for _ in range(3)]
+            for i in range(args.profile_calls):
+                w = ws[i % 4]
+                paged_attention_decode_batched(w.q, w.k_cache, w.v_cache, w.block_tables,
+                                               w.seq_lens, w.scale)
+            torch.cuda.synchronize()
+            log(f"profiled {name}: {args.profile_calls} calls")
+            del ws, base
+            torch.cuda.empty_cache()
+        return
     if args.reference_grid:
         print(json.dumps({"reference_grid": reference_grid(dev)}), flush=True)
         return
