@@ -639,6 +639,38 @@ def window_calls(copies, calls, warmup=5):
     return a.elapsed_time(b) / calls
 
 
+def window_write_calls(copies, calls, warmup=5):
+    """As window_calls, for the decode layer's write and attention together: each call writes
+    every sequence's new K/V row and attends (paged_decode_kv_write_attention; one launch on
+    the one-workgroup-per-pair schedule, the K/V write launch plus the attention launch
+    otherwise). The rows land in the rotated copies' pools at each sequence's last position."""
+    import torch
+
+    from engine.kernels.paged_attention_integration import paged_decode_kv_write_attention
+
+    w0 = copies[0]
+    g = torch.Generator(device=w0.q.device).manual_seed(17)
+    shape = (w0.num_seqs, w0.k_cache.shape[2], w0.k_cache.shape[3])
+    nk = torch.randn(shape, generator=g, device=w0.q.device).half()
+    nv = torch.randn(shape, generator=g, device=w0.q.device).half()
+
+    def call(w):
+        return paged_decode_kv_write_attention(w.q, nk, nv, w.k_cache, w.v_cache,
+                                               w.block_tables, w.seq_lens, w.scale)
+
+    for i in range(warmup):
+        call(copies[i % len(copies)])
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda._sleep(window_lead_cycles(calls))
+    a.record()
+    for i in range(calls):
+        call(copies[i % len(copies)])
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / calls
+
+
 def time_calls(copies, calls, warmup=5, lead_cycles=0, host_us=None):
     """HIP-event durations (ms) of `calls` attention calls rotating over the pool copies.
 
@@ -677,7 +709,8 @@ def config_timings(dev, seed, copies=4, calls=50):
 
     `us_mean` (and gbps, pct_of_hbm_peak) is the headline's statistic: `calls` calls enqueued
     back to back between one HIP event pair, behind a GPU busy-wait that lets the host queue
-    them first, so the window holds device time only. Beside it, per-call event pairs (each
+    them first, so the window holds device time only. `kv_write_attention_us_mean`: the same
+    for the decode layer's K/V write and attention as one call. Beside them, per-call event pairs (each
     call behind its own busy-wait; the pair adds a few microseconds of marker processing):
     `us_mean_per_call_events`, `us_median_per_call_events`; the host's time per call
     (`host_enqueue_us_median`), and the same calls issued back to back without the lead
@@ -698,6 +731,7 @@ def config_timings(dev, seed, copies=4, calls=50):
         ws += [clone_workload(ws[0]) for _ in range(copies - 1)]
         host = []
         win = window_calls(ws, calls)
+        fused = window_write_calls(ws, calls)
         ms = time_calls(ws, calls, lead_cycles=LEAD_CYCLES, host_us=host)
         nbytes = ws[0].algorithmic_bytes(unique=True)
         mean, med = statistics.fmean(ms), statistics.median(ms)
@@ -707,6 +741,7 @@ def config_timings(dev, seed, copies=4, calls=50):
                      "us_mean": round(win * 1e3, 2),
                      "gbps": round(nbytes / (win * 1e-3) / 1e9, 1),
                      "pct_of_hbm_peak": round(100 * nbytes / (win * 1e-3) / 1e9 / HBM_PEAK_GBS, 2),
+                     "kv_write_attention_us_mean": round(fused * 1e3, 2),
                      "us_mean_per_call_events": round(mean * 1e3, 2),
                      "us_median_per_call_events": round(med * 1e3, 2),
                      "calls": calls, "pool_copies_rotated": copies,

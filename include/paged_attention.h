@@ -54,7 +54,8 @@ enum {
  * 7: residual input of pa_rmsnorm_f16, pa_top2_f16; 8: pa_linear_f16; 9: pa_linear_f16
  * removed, decode workspace sizes stated per current device; 10:
  * pa_decode_batched_noalloc_f16; 11: pa_decode_rope_batched_f16, decode workspace
- * with room for shared-prefix records; 12: pa_decode_batched_schedule). */
+ * with room for shared-prefix records; 12: pa_decode_batched_schedule; 13:
+ * pa_decode_kv_write_batched_f16). */
 PA_API int pa_abi_version(void);
 
 /* Message of the last failed call on this thread ("" after a success). */
@@ -97,6 +98,42 @@ PA_API int pa_decode_batched_f16(const void* q, const int64_t q_strides[3],
                           int block_size, int num_blocks, int max_blocks_per_seq,
                           float scale, void* workspace, size_t workspace_bytes,
                           void* stream);
+
+/*
+ * The per-layer work of a decode step without the rotary embedding: the new
+ * token's K/V write into its block followed by pa_decode_batched_f16. Replaces
+ * the K/V write loop of paged_decode_attention_forward and the
+ * paged_attention_decode_batched call after it
+ * (engine/kernels/paged_attention_integration.py:148-161, :164-171). key and
+ * value are [num_seqs, num_kv_heads, head_dim] rows with unit head_dim stride,
+ * 8-element aligned strides and 16-byte aligned bases; row b is written to
+ * position seq_lens[b] - 1 (block block_tables[b][(L-1) / block_size], row
+ * (L-1) % block_size; skipped for L <= 0 or a slot outside the table or the
+ * pool) and attended over with the other L - 1 tokens. The same results (the
+ * same bits) as pa_kv_write_f16 followed by pa_decode_batched_f16 on the same
+ * stream. One launch where the batch takes one workgroup per (sequence,
+ * kv-head group) pair at head_dim 64 or 128 and block size 16 or 32 (the
+ * decode step's shapes); otherwise those two launches. Workspace: as for
+ * pa_decode_batched_f16 (pa_decode_batched_workspace_bytes). As for every
+ * fused write here, a slot whose block id lies outside the pool is not
+ * written, and the one-launch form then attends over the new rows where the
+ * two-launch form reads the clamped block's row (a malformed table either
+ * way); no other sequence may read the written slot in the same call (the
+ * reference refuses to write a block with more than one reference,
+ * engine/kernels/paged_attention_integration.py:587-592).
+ */
+PA_API int pa_decode_kv_write_batched_f16(const void* q, const int64_t q_strides[3],
+                                          const void* key, const int64_t key_strides[3],
+                                          const void* value, const int64_t value_strides[3],
+                                          void* k_cache, const int64_t k_strides[4],
+                                          void* v_cache, const int64_t v_strides[4],
+                                          const int32_t* block_tables,
+                                          const int64_t bt_strides[2], const int32_t* seq_lens,
+                                          void* out, const int64_t out_strides[3], int num_seqs,
+                                          int num_q_heads, int num_kv_heads, int head_dim,
+                                          int block_size, int num_blocks, int max_blocks_per_seq,
+                                          float scale, void* workspace, size_t workspace_bytes,
+                                          void* stream);
 
 /* Workspace the call above needs for these sizes (0 is a valid answer), on the
  * current HIP device: the schedule, and so the size, depends on that device's

@@ -324,7 +324,7 @@ using namespace pa;
 
 extern "C" {
 
-int pa_abi_version(void) { return 12; }
+int pa_abi_version(void) { return 13; }
 
 const char* pa_last_error(void) { return g_error.c_str(); }
 
@@ -391,6 +391,42 @@ int pa_decode_batched_f16(const void* q, const int64_t q_strides[3], const void*
                             scale, workspace, workspace_bytes, nullptr, stream);
 }
 
+int pa_decode_kv_write_batched_f16(const void* q, const int64_t q_strides[3], const void* key,
+                                   const int64_t key_strides[3], const void* value,
+                                   const int64_t value_strides[3], void* k_cache,
+                                   const int64_t k_strides[4], void* v_cache,
+                                   const int64_t v_strides[4], const int32_t* block_tables,
+                                   const int64_t bt_strides[2], const int32_t* seq_lens,
+                                   void* out, const int64_t out_strides[3], int num_seqs,
+                                   int num_q_heads, int num_kv_heads, int head_dim,
+                                   int block_size, int num_blocks, int max_blocks_per_seq,
+                                   float scale, void* workspace, size_t workspace_bytes,
+                                   void* stream) {
+  clear_error();
+  if (num_seqs > 0 && (!key || !value || !key_strides || !value_strides)) {
+    set_error("null pointer argument");
+    return PA_ERR_ARG;
+  }
+  if (num_seqs > 0 && (key_strides[2] != 1 || value_strides[2] != 1 || key_strides[0] % 8 ||
+                       key_strides[1] % 8 || value_strides[0] % 8 || value_strides[1] % 8 ||
+                       !aligned(key, 16) || !aligned(value, 16))) {
+    set_error("key/value rows need unit head_dim stride, 8-element aligned strides and 16-byte "
+              "aligned bases");
+    return PA_ERR_ARG;
+  }
+  RopeIn r{};
+  r.key = (const f16*)key;
+  r.ks_b = num_seqs > 0 ? key_strides[0] : 0;
+  r.ks_h = num_seqs > 0 ? key_strides[1] : 0;
+  r.val = (const f16*)value;
+  r.vs_b = num_seqs > 0 ? value_strides[0] : 0;
+  r.vs_h = num_seqs > 0 ? value_strides[1] : 0;
+  return pa::decode_batched(q, q_strides, k_cache, k_strides, v_cache, v_strides, block_tables,
+                            bt_strides, seq_lens, out, out_strides, num_seqs, num_q_heads,
+                            num_kv_heads, head_dim, block_size, num_blocks, max_blocks_per_seq,
+                            scale, workspace, workspace_bytes, nullptr, stream, &r);
+}
+
 }  // extern "C"
 
 namespace pa {
@@ -401,7 +437,8 @@ int decode_batched(const void* q, const int64_t q_strides[3], const void* k_cach
                    const int32_t* seq_lens, void* out, const int64_t out_strides[3],
                    int num_seqs, int num_q_heads, int num_kv_heads, int head_dim,
                    int block_size, int num_blocks, int max_blocks_per_seq, float scale,
-                   void* workspace, size_t workspace_bytes, ScratchFn scratch, void* stream) {
+                   void* workspace, size_t workspace_bytes, ScratchFn scratch, void* stream,
+                   const RopeIn* newrow) {
   if (num_seqs < 0) {
     set_error("num_seqs must be >= 0");
     return PA_ERR_ARG;
@@ -466,12 +503,26 @@ int decode_batched(const void* q, const int64_t q_strides[3], const void* k_cach
   a.split_tiles = st;
   a.max_splits = (int)ms;
   a.scale_log2 = scale * kLog2e;
+  // The new token's rows as a K/V write launch ahead of the attention launch.
+  auto write_first = [&]() -> int {
+    const int64_t ks[3] = {newrow->ks_b, newrow->ks_h, 1};
+    const int64_t vs[3] = {newrow->vs_b, newrow->vs_h, 1};
+    const int rc = pa_kv_write_f16(newrow->key, ks, newrow->val, vs, const_cast<void*>(k_cache),
+                                   k_strides, const_cast<void*>(v_cache), v_strides, block_tables,
+                                   bt_strides, seq_lens, 0, num_seqs, num_kv_heads, head_dim,
+                                   block_size, num_blocks, max_blocks_per_seq, stream);
+    return rc;
+  };
   if (!streamk) {
     const size_t need = pa_decode_batched_workspace_bytes(num_seqs, num_q_heads, num_kv_heads,
                                                           head_dim, block_size, max_blocks_per_seq);
     if (need && (!workspace || workspace_bytes < need)) {
       set_error("workspace of %zu bytes needed, %zu given", need, workspace_bytes);
       return PA_ERR_WORKSPACE;
+    }
+    if (newrow) {
+      const int rc = write_first();
+      if (rc) return rc;
     }
     return finish_launch(launch_decode_split(a, head_dim, num_seqs, (hipStream_t)stream));
   }
@@ -498,6 +549,17 @@ int decode_batched(const void* q, const int64_t q_strides[3], const void* k_cach
         num_seqs, num_q_heads, num_kv_heads, head_dim, block_size, max_blocks_per_seq);
     set_error("workspace of %zu bytes needed, %zu given", reserve, workspace_bytes);
     return PA_ERR_WORKSPACE;
+  }
+  if (newrow) {
+    if (decode_write_supported(a, head_dim)) {
+      a.cnt = (int*)workspace;
+      a.recs = (float*)((char*)workspace + kSkCounterBytes);
+      const size_t rb = workspace_bytes - kSkCounterBytes;
+      a.recs_bytes = rb < 0x7fffffffu ? (int)rb : 0x7fffffff;
+      return finish_launch(launch_decode_write(a, *newrow, head_dim, (hipStream_t)stream));
+    }
+    const int rc = write_first();
+    if (rc) return rc;
   }
   return finish_launch(launch_streamk_planned(a, head_dim, workspace, workspace_bytes,
                                               (hipStream_t)stream));

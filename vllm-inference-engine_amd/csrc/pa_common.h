@@ -203,13 +203,19 @@ typedef int (*ScratchFn)(void** ptr, hipStream_t stream);
 // `scratch` set, the workspace is not the caller's: workspace_bytes is the
 // size of the buffer `scratch` supplies, and calls that need more than that,
 // or the fixed-split path, are refused.
+struct RopeIn;
+// With `newrow` set, the call first writes each sequence's new token (its key
+// and value rows, newrow->key / newrow->val, at position seq_lens[b] - 1) into
+// the pool -- in the attention launch itself where the planned kernel supports
+// it, else as a K/V write launch before it.
 int decode_batched(const void* q, const int64_t q_strides[3], const void* k_cache,
                    const int64_t k_strides[4], const void* v_cache, const int64_t v_strides[4],
                    const int32_t* block_tables, const int64_t bt_strides[2],
                    const int32_t* seq_lens, void* out, const int64_t out_strides[3],
                    int num_seqs, int num_q_heads, int num_kv_heads, int head_dim,
                    int block_size, int num_blocks, int max_blocks_per_seq, float scale,
-                   void* workspace, size_t workspace_bytes, ScratchFn scratch, void* stream);
+                   void* workspace, size_t workspace_bytes, ScratchFn scratch, void* stream,
+                   const RopeIn* newrow = nullptr);
 
 // Launchers (defined next to their kernels).
 hipError_t launch_decode_split(const DecodeArgs& a, int D, int num_seqs, hipStream_t s);
@@ -241,6 +247,16 @@ struct RopeIn {
 // launcher.
 bool pair_rope_supported(const DecodeArgs& a, int D);
 hipError_t launch_decode_pair_rope(const DecodeArgs& a, const RopeIn& r, int D, hipStream_t s);
+// Whether the attention kernel with the K/V write in the same launch serves
+// the launch planned in `a` (one workgroup per pair, head_dim 64 or 128,
+// block 16 or 32; key and value rows in r.key / r.val, 16-byte aligned), and
+// its launcher. Stream-K launches take the K/V write as a launch of its own:
+// measured on MI355X at batch 256 x lognormal ~4.6k tokens, the write state
+// inside decode_streamk_kernel (new rows substituted while staging, the slot
+// written after the merge) cost 112.9 us per step against 100.9 us for the two
+// launches (register spills in the segment walk).
+bool decode_write_supported(const DecodeArgs& a, int D);
+hipError_t launch_decode_write(const DecodeArgs& a, const RopeIn& r, int D, hipStream_t s);
 hipError_t launch_prefill_attn(const PrefillAttnArgs& a, int D, hipStream_t s);
 hipError_t launch_rmsnorm(const f16* x, int64_t xs, const f16* res, int64_t rs, f16* sum,
                           int64_t ss, const f16* w, f16* y, int64_t ys, int rows, int H,

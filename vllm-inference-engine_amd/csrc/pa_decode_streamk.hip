@@ -120,7 +120,8 @@ __device__ inline int block_excl_sum(int (&v)[PER], int* s_tot, int lane, int wa
 // token L - 1 are taken from nrow instead of the pool: a decode step's new
 // token, whose write into the pool need not have landed. pre_loop() runs in
 // every wavefront after the first chunks' loads are issued, before any is
-// staged or computed (nrow and qf must be complete when it returns).
+// staged or computed (nrow's rows and qf must be complete when it returns;
+// nrow is read through the caller's variable, which pre_loop may clear).
 struct SegEnd {
   int s1, L;
 };
@@ -140,7 +141,7 @@ __device__ __forceinline__ void stream_tiles(const DecodeArgs& a, const int32_t*
                                              const f16x8 (&qf)[NCB][D / 32], f16* kst, f16* vst,
                                              int wave, int lane, float (&m_run)[NCB],
                                              float (&l_run)[NCB], f32x4 (&acc)[NCB][D / 16],
-                                             const f16* nrow = nullptr,
+                                             const f16* const& nrow = nullptr,
                                              PreLoop pre_loop = PreLoop{}) {
   constexpr int NC = D / 32;
   constexpr int ND = D / 16;
@@ -1173,8 +1174,11 @@ struct PairSeg {
   const int32_t* len;  // nullptr: every sequence has uniform_len tokens
   int uniform_len, cap;
   int& L_out;
+  int& Lraw_out;  // the length as given (a write past the table is skipped)
   __device__ SegEnd operator()() const {
-    const int L = min(max(len ? load_uniform(len) : uniform_len, 0), cap);
+    const int Lraw = len ? load_uniform(len) : uniform_len;
+    const int L = min(max(Lraw, 0), cap);
+    Lraw_out = Lraw;
     L_out = L;
     return {(L + 15) >> 4, L};
   }
@@ -1187,16 +1191,19 @@ struct PairSeg {
 // the block ids of its first chunks, the query rows and, with ROPE, the new
 // token's key and value rows and the rotary cos / sin rows.
 //
-// ROPE (the fused decode-layer form): q and the new key arrive unrotated;
-// the kernel rotates them (rope8), attends over the L tokens with the new
-// token's rotated key and value substituted for the pool's rows at position
-// L - 1, and writes them into that slot of the pool -- the work of
+// NEWROW 2, ROPE (the fused decode-layer form): q and the new key arrive
+// unrotated; the kernel rotates them (rope8), attends over the L tokens with
+// the new token's rotated key and value substituted for the pool's rows at
+// position L - 1, and writes them into that slot of the pool -- the work of
 // rope_kv_write_kernel followed by this kernel without it, in one launch. The
 // write is issued at the end: no workgroup but this one reads the pair's
-// rows during the launch.
-template <int D, int NT, int BS, int HG, int NW, bool ROPE>
+// rows during the launch. NEWROW 1: the same without the rotation (the K/V
+// write followed by this kernel); NEWROW 0: attention only.
+template <int D, int NT, int BS, int HG, int NW, int NEWROW>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void decode_pair_kernel(DecodeArgs a, RopeIn r) {
+  constexpr bool ROPE = NEWROW == 2;
+  constexpr bool WRITE = NEWROW != 0;
   constexpr int NC = D / 32;
   constexpr int ND = D / 16;
   constexpr int LS = D + 8;
@@ -1205,7 +1212,7 @@ void decode_pair_kernel(DecodeArgs a, RopeIn r) {
   constexpr int WAVE_BYTES = 2 * VST * 2 > CMB * 4 ? 2 * VST * 2 : CMB * 4;
   static_assert(!ROPE || D >= 64, "rotation pairs must lie in one lane's query fragments");
   __shared__ __attribute__((aligned(16))) char smem[NW * WAVE_BYTES];
-  __shared__ __attribute__((aligned(16))) f16 s_new[ROPE ? 2 * HG * D : 8];  // new K rows, then V rows
+  __shared__ __attribute__((aligned(16))) f16 s_new[WRITE ? 2 * HG * D : 8];  // new K rows, then V rows
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1247,27 +1254,29 @@ void decode_pair_kernel(DecodeArgs a, RopeIn r) {
     }
   }
 
-  // ROPE: the new token's key and value rows. Lane t < HG * D / 16 of the
+  // WRITE: the new token's key and value rows. Lane t < HG * D / 16 of the
   // first wavefront takes 8 elements j of one head and their partners
-  // j + D / 2; the rotated key and the value go to s_new.
+  // j + D / 2; the key (rotated with ROPE) and the value go to s_new.
   constexpr int NRL = HG * D / 16;
   f16x8 nk1, nk2, nv1, nv2, nc1, nc2, ns1, ns2;
-  if constexpr (ROPE) {
+  if constexpr (WRITE) {
     if (tid < NRL) {
       const int hg = tid / (D / 16);
       const int j = (tid - hg * (D / 16)) * 8;
       const f16* kp = r.key + (int64_t)b * r.ks_b + (int64_t)(h0 + hg) * r.ks_h;
       const f16* vp = r.val + (int64_t)b * r.vs_b + (int64_t)(h0 + hg) * r.vs_h;
-      const f16* cp = r.cos + (int64_t)b * r.cs_b;
-      const f16* sp = r.sin + (int64_t)b * r.ss_b;
       nk1 = *reinterpret_cast<const f16x8*>(kp + j);
       nk2 = *reinterpret_cast<const f16x8*>(kp + j + D / 2);
       nv1 = *reinterpret_cast<const f16x8*>(vp + j);
       nv2 = *reinterpret_cast<const f16x8*>(vp + j + D / 2);
-      nc1 = *reinterpret_cast<const f16x8*>(cp + j);
-      nc2 = *reinterpret_cast<const f16x8*>(cp + j + D / 2);
-      ns1 = *reinterpret_cast<const f16x8*>(sp + j);
-      ns2 = *reinterpret_cast<const f16x8*>(sp + j + D / 2);
+      if constexpr (ROPE) {
+        const f16* cp = r.cos + (int64_t)b * r.cs_b;
+        const f16* sp = r.sin + (int64_t)b * r.ss_b;
+        nc1 = *reinterpret_cast<const f16x8*>(cp + j);
+        nc2 = *reinterpret_cast<const f16x8*>(cp + j + D / 2);
+        ns1 = *reinterpret_cast<const f16x8*>(sp + j);
+        ns2 = *reinterpret_cast<const f16x8*>(sp + j + D / 2);
+      }
     }
   }
   // The length is loaded after the first block ids are issued (they do not
@@ -1275,29 +1284,37 @@ void decode_pair_kernel(DecodeArgs a, RopeIn r) {
   // tokens streams no tile: every wavefront keeps an empty state and the
   // merge writes rows of zeros.
   int L = 0;
+  int Lraw = 0;
+  // The rows substituted for the pool's at position L - 1; cleared when the
+  // given length puts the new token's slot past the table (no write then, as
+  // in rope_kv_write_kernel, so the pool's row is read).
+  const f16* nrow = WRITE ? s_new : nullptr;
   // Runs in every wavefront once the first chunks' loads are in flight (the
-  // length known): with ROPE it also fetches the block id of the new token's
+  // length known): with WRITE it also fetches the block id of the new token's
   // slot, position L - 1, for the write at the end.
   int slot_id = -1;
   auto rotate = [&]() {
-    if constexpr (ROPE) {
+    if constexpr (WRITE) {
       const int lb = (L - 1) / a.bs;
-      if (L > 0 && lb < a.max_blocks)
+      if (Lraw > a.max_blocks * a.bs) nrow = nullptr;
+      else if (L > 0 && lb < a.max_blocks)
         slot_id = load_uniform(a.bt + (int64_t)b * a.bt_sb + (int64_t)lb * a.bt_sk);
+      if constexpr (ROPE) {
 #pragma unroll
-      for (int hg = 0; hg < HG; ++hg) {
+        for (int hg = 0; hg < HG; ++hg) {
 #pragma unroll
-        for (int c = 0; c < NC / 2; ++c)
-          rope8(qf[hg][c], qf[hg][c + NC / 2], qc[c], qc[c + NC / 2], qs[c], qs[c + NC / 2],
-                qf[hg][c], qf[hg][c + NC / 2]);
+          for (int c = 0; c < NC / 2; ++c)
+            rope8(qf[hg][c], qf[hg][c + NC / 2], qc[c], qc[c + NC / 2], qs[c], qs[c + NC / 2],
+                  qf[hg][c], qf[hg][c + NC / 2]);
 #pragma unroll
-        for (int c = 0; c < NC; ++c)
-          if (row >= a.g) qf[hg][c] = zero8();
+          for (int c = 0; c < NC; ++c)
+            if (row >= a.g) qf[hg][c] = zero8();
+        }
       }
       if (tid < NRL) {
         const int hg = tid / (D / 16);
         const int j = (tid - hg * (D / 16)) * 8;
-        rope8(nk1, nk2, nc1, nc2, ns1, ns2, nk1, nk2);
+        if constexpr (ROPE) rope8(nk1, nk2, nc1, nc2, ns1, ns2, nk1, nk2);
         *reinterpret_cast<f16x8*>(&s_new[hg * D + j]) = nk1;
         *reinterpret_cast<f16x8*>(&s_new[hg * D + j + D / 2]) = nk2;
         *reinterpret_cast<f16x8*>(&s_new[(HG + hg) * D + j]) = nv1;
@@ -1307,7 +1324,7 @@ void decode_pair_kernel(DecodeArgs a, RopeIn r) {
     }
   };
 
-  PairSeg seg{a.lens ? a.lens + b : nullptr, a.uniform_len, a.max_blocks * a.bs, L};
+  PairSeg seg{a.lens ? a.lens + b : nullptr, a.uniform_len, a.max_blocks * a.bs, L, Lraw};
 
   f16* kst = reinterpret_cast<f16*>(smem + wave * WAVE_BYTES);
   float m_run[HG], l_run[HG];
@@ -1321,7 +1338,7 @@ void decode_pair_kernel(DecodeArgs a, RopeIn r) {
   }
   stream_tiles<D, BS, HG, HG, NT, false, NW>(a, a.bt + (int64_t)b * a.bt_sb, h0, 0, seg, HG, qf,
                                              kst, kst + VST, wave, lane, m_run, l_run, acc,
-                                             ROPE ? s_new : nullptr, rotate);
+                                             nrow, rotate);
   merge_waves<D, HG, NW>(smem, WAVE_BYTES, wave, lane, m_run, l_run, acc, HG,
                          [&](int hg, int nd, float, float den, f32x4 num) {
     if (row < a.g) {
@@ -1334,11 +1351,11 @@ void decode_pair_kernel(DecodeArgs a, RopeIn r) {
     }
   });
 
-  if constexpr (ROPE) {
+  if constexpr (WRITE) {
     // The new token's slot: position L - 1, in the block the table lists for
     // it; a slot outside the table or the pool is not written (as in
     // rope_kv_write_kernel), nor is anything for a sequence with no tokens.
-    if (tid < NRL && L > 0) {
+    if (tid < NRL && L > 0 && nrow != nullptr) {
       const int pos = L - 1;
       const int lb = pos / a.bs;
       const int id = slot_id;
@@ -1383,7 +1400,7 @@ template <int D, int BS, int HG>
 hipError_t launch_sk(const DecodeArgs& a, hipStream_t s) {
   constexpr int NT = sk_chunk_tiles<D>(HG);
   if (a.pair_per_wg)
-    decode_pair_kernel<D, NT, BS, HG, kSkWaves, false><<<a.num_wg, 64 * kSkWaves, 0, s>>>(a, RopeIn{});
+    decode_pair_kernel<D, NT, BS, HG, kSkWaves, 0><<<a.num_wg, 64 * kSkWaves, 0, s>>>(a, RopeIn{});
   else
     decode_streamk_kernel<D, NT, BS, HG, kSkWaves><<<a.num_wg, 64 * kSkWaves, 0, s>>>(a);
   return hipGetLastError();
@@ -1392,7 +1409,16 @@ hipError_t launch_sk(const DecodeArgs& a, hipStream_t s) {
 template <int D, int BS, int HG>
 hipError_t launch_pair_rope(const DecodeArgs& a, const RopeIn& r, hipStream_t s) {
   constexpr int NT = sk_chunk_tiles<D>(HG);
-  decode_pair_kernel<D, NT, BS, HG, kSkWaves, true><<<a.num_wg, 64 * kSkWaves, 0, s>>>(a, r);
+  decode_pair_kernel<D, NT, BS, HG, kSkWaves, 2><<<a.num_wg, 64 * kSkWaves, 0, s>>>(a, r);
+  return hipGetLastError();
+}
+
+// Attention with the new token's K/V write in the same launch (one workgroup
+// per pair).
+template <int D, int BS, int HG>
+hipError_t launch_write(const DecodeArgs& a, const RopeIn& r, hipStream_t s) {
+  constexpr int NT = sk_chunk_tiles<D>(HG);
+  decode_pair_kernel<D, NT, BS, HG, kSkWaves, 1><<<a.num_wg, 64 * kSkWaves, 0, s>>>(a, r);
   return hipGetLastError();
 }
 
@@ -1438,6 +1464,21 @@ hipError_t launch_decode_pair_rope(const DecodeArgs& a, const RopeIn& r, int D, 
     return a.bs == 16 ? launch_pair_rope<64, 16, 1>(a, r, s) : launch_pair_rope<64, 32, 1>(a, r, s);
   }
   return a.bs == 16 ? launch_pair_rope<128, 16, 1>(a, r, s) : launch_pair_rope<128, 32, 1>(a, r, s);
+}
+
+bool decode_write_supported(const DecodeArgs& a, int D) {
+  return a.pair_per_wg && (D == 64 || D == 128) && (a.bs == 16 || a.bs == 32) &&
+         tile_offsets_fit(a, D, a.head_group) && (a.head_group == 1 || D == 64);
+}
+
+hipError_t launch_decode_write(const DecodeArgs& a, const RopeIn& r, int D, hipStream_t s) {
+  if (!decode_write_supported(a, D)) return hipErrorInvalidValue;
+  if (D == 64) {
+    if (a.head_group == 2)
+      return a.bs == 16 ? launch_write<64, 16, 2>(a, r, s) : launch_write<64, 32, 2>(a, r, s);
+    return a.bs == 16 ? launch_write<64, 16, 1>(a, r, s) : launch_write<64, 32, 1>(a, r, s);
+  }
+  return a.bs == 16 ? launch_write<128, 16, 1>(a, r, s) : launch_write<128, 32, 1>(a, r, s);
 }
 
 // Kv heads a wavefront handles together for this shape.

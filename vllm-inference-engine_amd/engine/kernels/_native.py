@@ -17,7 +17,7 @@ import torch  # noqa: F401  (must be loaded before the HIP library, see above)
 
 LIB_NAME = "libpa_gfx950.so"
 LIB_PATH = Path(__file__).with_name(LIB_NAME)
-ABI_VERSION = 12
+ABI_VERSION = 13
 
 PA_OK = 0
 PA_ERR_ARG = 1
@@ -40,6 +40,9 @@ SIGNATURES: dict[str, tuple] = {
         _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _vp, _i64p,
         _i32, _i32, _i32, _i32, _i32, _i32, _i32, _f32, _vp, _sz, _vp]),
     "pa_decode_batched_workspace_bytes": (_sz, [_i32, _i32, _i32, _i32, _i32, _i32]),
+    "pa_decode_kv_write_batched_f16": (_i32, [
+        _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _vp, _i64p,
+        _i32, _i32, _i32, _i32, _i32, _i32, _i32, _f32, _vp, _sz, _vp]),
     "pa_decode_batched_schedule": (_i32, [_i32, _i32, _i32, _i32, _i32, _i32,
                                           ctypes.POINTER(ctypes.c_int)]),
     "pa_decode_v2_f16": (_i32, [

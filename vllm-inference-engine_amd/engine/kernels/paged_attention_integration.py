@@ -50,6 +50,7 @@ __all__ = [
     "paged_kv_write",
     "paged_rope_kv_write",
     "paged_rope_decode_attention",
+    "paged_decode_kv_write_attention",
     "paged_prefill_copy",
     "paged_decode_attention_forward",
     "paged_prefill_attention_forward",
@@ -279,6 +280,84 @@ def paged_rope_decode_attention(
             stream)
     _native.check(status, "pa_decode_rope_batched_f16")
     return out
+
+
+def _rows16(x: torch.Tensor) -> torch.Tensor:
+    """Rows with unit head_dim stride, 8-element aligned strides and a 16-byte aligned base."""
+    ok = (x.stride(-1) == 1 and all(st % 8 == 0 for st in x.stride()[:-1])
+          and x.data_ptr() % 16 == 0)
+    return x if ok else x.contiguous()
+
+
+def paged_decode_kv_write_attention(
+    query: torch.Tensor,         # [num_seqs, num_q_heads, head_dim] (or [B, Hq, 1, D])
+    key: torch.Tensor,           # [num_seqs, num_kv_heads, head_dim] (or [B, Hkv, 1, D])
+    value: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    block_tables: torch.Tensor,  # [num_seqs, max_blocks] int32
+    seq_lens: torch.Tensor,      # [num_seqs] int32, counting the new token
+    scale: float,
+) -> torch.Tensor:
+    """The new token's K/V write followed by batched paged attention, in one launch.
+
+    The reference's K/V write loop and the paged_attention_decode_batched call
+    after it (integration.py:148-161, :164-171): key/value row b goes to
+    position seq_lens[b] - 1 of sequence b, then every query attends over its
+    seq_lens[b] tokens, the new one included. The same bits as paged_kv_write
+    followed by paged_attention_decode_batched; one kernel launch where the
+    batch takes one workgroup per (sequence, kv-head group) pair at head_dim
+    64 or 128 with blocks of 16 or 32 tokens (the decode step's shapes), else
+    those two launches.
+    Returns [num_seqs, num_q_heads, head_dim]; asynchronous on the current stream.
+    """
+    query = _as_rows(query)
+    key = _as_rows(key)
+    value = _as_rows(value)
+    for t in (query, key, value, k_cache, v_cache):
+        assert t.is_cuda and t.dtype == torch.float16
+    assert block_tables.dtype == torch.int32 and block_tables.is_cuda and block_tables.dim() == 2
+    assert seq_lens.is_cuda and seq_lens.dtype == torch.int32
+    _native.same_device(query, key, value, k_cache, v_cache, block_tables, seq_lens)
+    assert k_cache.shape == v_cache.shape, "k_cache and v_cache must have the same shape"
+    num_blocks, block_size, num_kv_heads, head_dim = k_cache.shape
+    num_seqs, num_q_heads = query.shape[0], query.shape[1]
+    assert query.shape[2] == head_dim, f"Head dimensions must match: {query.shape[2]} vs {head_dim}"
+    assert num_q_heads % num_kv_heads == 0, (
+        f"num_q_heads ({num_q_heads}) must be divisible by num_kv_heads ({num_kv_heads})")
+    assert key.shape == (num_seqs, num_kv_heads, head_dim) and value.shape == key.shape
+    assert block_tables.shape[0] == num_seqs and seq_lens.shape == (num_seqs,)
+    out = torch.empty((num_seqs, num_q_heads, head_dim), dtype=torch.float16, device=query.device)
+    if num_seqs == 0:
+        return out
+    assert block_tables.shape[1] > 0, "block_tables needs at least one column"
+    query, key, value = _rows16(query), _rows16(key), _rows16(value)
+    lib = _native.load()
+    dev = query.device
+    max_blocks = block_tables.shape[1]
+    ws_key = (dev.index, num_seqs, num_q_heads, num_kv_heads, head_dim, block_size, max_blocks)
+    stream = _native.stream_handle(dev)
+    with _on_device(dev):
+        ws_bytes = _write_ws_sizes.get(ws_key)
+        if ws_bytes is None:
+            ws_bytes = _write_ws_sizes[ws_key] = lib.pa_decode_batched_workspace_bytes(
+                *ws_key[1:])
+        status = lib.pa_decode_kv_write_batched_f16(
+            query.data_ptr(), _native.strides_of(query),
+            key.data_ptr(), _native.strides_of(key),
+            value.data_ptr(), _native.strides_of(value),
+            k_cache.data_ptr(), _native.strides_of(k_cache),
+            v_cache.data_ptr(), _native.strides_of(v_cache),
+            block_tables.data_ptr(), _native.strides_of(block_tables),
+            seq_lens.data_ptr(), out.data_ptr(), _native.strides_of(out),
+            num_seqs, num_q_heads, num_kv_heads, head_dim, block_size, num_blocks, max_blocks,
+            float(scale), _native.workspace(ws_bytes, dev, stream, _native.WS_DECODE), ws_bytes,
+            stream)
+    _native.check(status, "pa_decode_kv_write_batched_f16")
+    return out
+
+
+_write_ws_sizes: dict = {}
 
 
 class PagedAttentionContext:
