@@ -60,11 +60,57 @@ def oracle_greedy(model, prompt, steps, forced=None):
 
 
 @torch.inference_mode()
-def paged_greedy(runner, prompts, steps, forced=None, keep=None):
+def oracle_greedy_batch(model, prompts, steps, chunk=32):
+    """oracle_greedy for many prompts at once: transformers' contiguous-cache decode with the
+    prompts left-padded into batches of `chunk` (attention mask and position ids skip the
+    padding). Returns each stream's greedy tokens and top-1/top-2 margins, and every step's
+    fp16 logits kept on the GPU, [steps, len(prompts), vocab]."""
+    dev = next(model.parameters()).device
+    n_seq = len(prompts)
+    vocab = model.config.vocab_size
+    logits_all = torch.empty(steps, n_seq, vocab, dtype=torch.float16, device=dev)
+    toks = [[] for _ in range(n_seq)]
+    margins = [[] for _ in range(n_seq)]
+    for c0 in range(0, n_seq, chunk):
+        idx = list(range(c0, min(n_seq, c0 + chunk)))
+        width = max(len(prompts[i]) for i in idx)
+        ids = torch.zeros(len(idx), width, dtype=torch.long)
+        mask = torch.zeros(len(idx), width, dtype=torch.long)
+        for r, i in enumerate(idx):
+            ids[r, width - len(prompts[i]):] = torch.tensor(prompts[i])
+            mask[r, width - len(prompts[i]):] = 1
+        ids, mask = ids.to(dev), mask.to(dev)
+        pos = (mask.cumsum(-1) - 1).clamp(min=0)
+        out = model(input_ids=ids, attention_mask=mask, position_ids=pos, use_cache=True)
+        pkv = out.past_key_values
+        logits = out.logits[:, -1]
+        last = pos[:, -1:]
+        for step in range(steps):
+            logits_all[step, idx[0]:idx[-1] + 1] = logits.half()
+            top2 = torch.topk(logits.float(), 2, dim=-1).values
+            tok = torch.argmax(logits, dim=-1)
+            for r, (t, m) in enumerate(zip(tok.tolist(), (top2[:, 0] - top2[:, 1]).tolist())):
+                toks[idx[r]].append(int(t))
+                margins[idx[r]].append(float(m))
+            if step + 1 == steps:
+                break
+            mask = torch.cat([mask, torch.ones_like(mask[:, :1])], dim=1)
+            last = last + 1
+            out = model(input_ids=tok[:, None], attention_mask=mask, position_ids=last,
+                        past_key_values=pkv, use_cache=True)
+            pkv = out.past_key_values
+            logits = out.logits[:, -1]
+    return toks, margins, logits_all
+
+
+@torch.inference_mode()
+def paged_greedy(runner, prompts, steps, forced=None, keep=None, on_logits=None):
     """Prefill each prompt, then batched decode steps; optional forced input tokens per sequence.
 
     Returns every sequence's tokens and the per-step logits (fp32, cpu) of the
-    sequences in `keep` (all of them when None; the others get None)."""
+    sequences in `keep` (all of them when None; the others get None). on_logits(step, seqs),
+    when given, is called after the prefill (step 0) and after every decode step, with each
+    sequence's `last_logits` still on the GPU."""
     from engine.memory.block_allocator import BlockTable
 
     bs = runner.block_size
@@ -83,11 +129,15 @@ def paged_greedy(runner, prompts, steps, forced=None, keep=None):
         seqs.append(seq)
     keep = set(range(len(seqs))) if keep is None else set(keep)
     logits = [[s.last_logits.float().cpu()] if i in keep else None for i, s in enumerate(seqs)]
+    if on_logits is not None:
+        on_logits(0, seqs)
     for step in range(1, steps):
         for s in seqs:  # the scheduler's job: a new block at each block boundary
             if s.block_table.num_tokens // bs >= len(s.block_table.physical_block_ids):
                 s.block_table.physical_block_ids.append(alloc.allocate())
         toks = runner.decode_step(seqs)
+        if on_logits is not None:
+            on_logits(step, seqs)
         for i, (s, t) in enumerate(zip(seqs, toks)):
             s.generated_ids.append(t)
             s.last_token_id = t if forced is None else forced[i][step]
@@ -178,13 +228,22 @@ def test_qwen05_decode_step_at_benchmark_size(cuda_device):
     Random-init Qwen2.5-0.5B architecture, batch 128, prompts U[64, 1024] of
     random token ids (the benchmark's seed), 128 greedy steps with captured
     graphs and fused decoder layers -- so every layer runs the batch-128
-    attention schedule the benchmark measures. 16 streams, the shortest and
-    longest prompts among them, are compared with transformers' own
-    DynamicCache decode of the same model: greedy streams must agree up to a
-    near-tie divergence (oracle top-1/top-2 margin < 0.05), and with the
-    oracle's tokens fed back (teacher forcing) every step's logits must be
-    within 0.1 (reference engine/kernels/paged_attention_integration.py:518-653,
+    attention schedule the benchmark measures. Oracle: transformers' own
+    DynamicCache decode of the same model (reference
+    engine/kernels/paged_attention_integration.py:518-653,
     tests/test_kernel_qwen_integration.py:30-123).
+
+    * Greedy streams, all 128: each must agree with the oracle's up to a
+      near-tie divergence (oracle top-1/top-2 margin < 0.05). The oracle runs
+      the prompts left-padded into batches of 32 so that all streams fit the
+      test's time.
+    * Teacher-forced logits (the oracle's tokens fed to both paths), within
+      0.1 at every step, on 16 streams (the shortest and the longest prompts
+      among them) against the oracle run one sequence at a time: the padded
+      batches are not that oracle's numerics -- on this workload they differ
+      from it by up to 0.13 on some streams, where the paged path agrees with
+      the one-sequence oracle -- so the padded oracle's logits are reported
+      for all 128 streams but gated only through the tokens.
     """
     from engine import workloads
     from engine.kernels.paged_attention_integration import KernelPagedManualDecode
@@ -204,24 +263,36 @@ def test_qwen05_decode_step_at_benchmark_size(cuda_device):
         return r
 
     got, _ = paged_greedy(runner(), prompts, steps, keep=())
-    forced = [list(t) for t in got]
-    divergences, oracle_logits = 0, {}
-    for i in checked:
-        want, logits, margins = oracle_greedy(model, prompts[i], steps)
-        oracle_logits[i] = logits
-        forced[i] = want
-        for j, (a, b) in enumerate(zip(got[i], want)):
+    want, margins, padded_logits = oracle_greedy_batch(model, prompts, steps)
+    divergences = 0
+    for i in range(batch):
+        for j, (a, b) in enumerate(zip(got[i], want[i])):
             if a != b:
                 divergences += 1
-                assert margins[j] < NEAR_TIE, (
+                assert margins[i][j] < NEAR_TIE, (
                     f"stream {i} (prompt {len(prompts[i])}) diverged at step {j} with oracle "
-                    f"margin {margins[j]:.4f} >= {NEAR_TIE}")
+                    f"margin {margins[i][j]:.4f} >= {NEAR_TIE}")
                 break
-    _, paged_logits = paged_greedy(runner(), prompts, steps, forced=forced, keep=checked)
+    # Teacher forcing on the padded oracle's tokens; the one-sequence oracle on the 16
+    # streams follows the same tokens.
+    oracle_logits = {}
+    for i in checked:
+        _, oracle_logits[i], _ = oracle_greedy(model, prompts[i], steps, forced=want[i])
+    worst_padded = torch.zeros((), device=cuda_device)
+
+    def compare(step, seqs):
+        nonlocal worst_padded
+        paged = torch.stack([s.last_logits for s in seqs]).float()
+        worst_padded = torch.maximum(worst_padded,
+                                     (paged - padded_logits[step].float()).abs().max())
+
+    _, paged_logits = paged_greedy(runner(), prompts, steps, forced=want, keep=checked,
+                                   on_logits=compare)
     worst = max((paged_logits[i] - oracle_logits[i]).abs().max().item() for i in checked)
-    print(f"[decode-step] batch {batch} x {steps} steps, {len(checked)} streams checked: "
-          f"{divergences} near-tie divergences, teacher-forced max |logit diff| {worst:.4f}",
-          flush=True)
+    print(f"[decode-step] batch {batch} x {steps} steps: all {batch} greedy streams checked, "
+          f"{divergences} near-tie divergences; teacher-forced max |logit diff| {worst:.4f} on "
+          f"{len(checked)} streams (one-sequence oracle), {worst_padded.item():.4f} on all "
+          f"{batch} (padded-batch oracle, reported)", flush=True)
     assert worst <= LOGIT_TOL
 
 
