@@ -77,7 +77,10 @@ def test_noalloc_inside_a_captured_graph(cuda_device):
     torch.cuda.synchronize()
     assert torch.equal(out, want)
     graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
+    # Inside inference mode, as the decode runner captures its steps: an earlier test's
+    # inference-mode work may have made torch's generator state an inference tensor, which
+    # capture_begin updates in place.
+    with torch.inference_mode(), torch.cuda.graph(graph):
         _noalloc(w, out)
     for i in range(3):
         out.zero_()
