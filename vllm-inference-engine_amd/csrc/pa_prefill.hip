@@ -185,6 +185,14 @@ __global__ __launch_bounds__(64 * NW) void prefill_attn_kernel(PrefillAttnArgs a
   fetch_ids(t0 + 1);
   stash(t0 & 1);
   __syncthreads();
+  // Every load issued so far (the query fragments included, which the
+  // compiler may place after the first tile's loads) is complete before the
+  // loop: otherwise the loop's wait counts must assume the query loads may
+  // still be pending at its first products, and every tile's score products
+  // would wait for the next tile's K/V loads issued just before them.
+  __builtin_amdgcn_sched_barrier(0);
+  __builtin_amdgcn_s_waitcnt(0);
+  __builtin_amdgcn_sched_barrier(0);
   for (int kt = t0; kt < t1; ++kt) {
     const bool more = kt + 1 < t1;
     if (more) {
