@@ -138,7 +138,37 @@ __global__ __launch_bounds__(64 * NW) void prefill_attn_kernel(PrefillAttnArgs a
   // (clamped, so every load is a valid pool row and no branch splits the
   // loads): their scores fall past every column's position and are masked,
   // and p = 0 times a finite row adds nothing.
+  //
+  // Tiles wholly below kmax, when the block size divides the key tile: a
+  // piece's row in the tile -- so its table column within the tile, its row in
+  // the block and its 16-byte column -- is the same in every tile, and only
+  // the block id changes. Its K and V addresses are then the block id times
+  // the block stride plus a base fixed for the piece, and its block-id address
+  // a fixed one plus a tile offset common to the workgroup: a few vector
+  // instructions per piece instead of the general form's clamps, divisions
+  // and two 64-bit multiply-adds per load.
+  constexpr bool FIXED = BS > 0 && KT % BS == 0 && D <= 128;  // at head_dim 256 the bases cost occupancy
+  const f16* kfix[PER];
+  const f16* vfix[PER];
+  const int32_t* idfix[PER];
+  if constexpr (FIXED) {
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int f = i * 64 * NW + tid;
+      const uint32_t r = (uint32_t)(f / CPR), c8 = (uint32_t)(f % CPR) * 8;
+      kfix[i] = kbase + ((r % BS) * k_st + c8);
+      vfix[i] = vbase + ((r % BS) * v_st + c8);
+      idfix[i] = btrow + (r / BS) * bt_sk;
+    }
+  }
+  auto whole = [&](int kt) { return FIXED && (kt + 1) * KT <= kmax; };  // workgroup-uniform
   auto fetch_ids = [&](int kt) {
+    if (whole(kt)) {
+      const uint32_t to = (uint32_t)kt * (uint32_t)(KT / (BS > 0 ? BS : 1)) * bt_sk;
+#pragma unroll
+      for (int i = 0; i < PER; ++i) ids[i] = idfix[i][to];
+      return;
+    }
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
       const int key = min(kt * KT + (i * 64 * NW + tid) / CPR, kmax - 1);
@@ -146,6 +176,15 @@ __global__ __launch_bounds__(64 * NW) void prefill_attn_kernel(PrefillAttnArgs a
     }
   };
   auto fetch_kv = [&](int kt) {
+    if (whole(kt)) {
+#pragma unroll
+      for (int i = 0; i < PER; ++i) {
+        const uint32_t id = (uint32_t)min(max(ids[i], 0), a.num_blocks - 1);
+        kr[i] = *reinterpret_cast<const u32x4*>(kfix[i] + (uint64_t)id * k_sb);
+        vr[i] = *reinterpret_cast<const u32x4*>(vfix[i] + (uint64_t)id * v_sb);
+      }
+      return;
+    }
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
       const int f = i * 64 * NW + tid;
