@@ -767,8 +767,8 @@ def config_timings(dev, seed, copies=4, calls=50):
 def main():
     args = parse_args()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build measures one GPU; --gpus must be 1 "
-                          "(the path would shard by sequence or kv head, see DESIGN.md)"}))
+        print(json.dumps({"error": "one GPU only; --gpus must be 1 (the path would shard by "
+                          "sequence or by kv head, each GPU running this kernel on its share)"}))
         raise SystemExit(2)
     import torch
 

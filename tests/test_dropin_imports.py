@@ -115,7 +115,7 @@ _REF_ALLOCATOR_STANDIN = textwrap.dedent('''
 
 
 def test_copied_kernels_bind_to_the_reference_tree(tmp_path):
-    """Route of INTEGRATION.md: copy engine/kernels/* over a tree laid out as the reference's."""
+    """The drop-in route: copy engine/kernels/* over a tree laid out as the reference's."""
     root = tmp_path / "reference_tree"
     for d in ("engine", "engine/kernels", "engine/memory", "engine/scheduler", "engine/serving"):
         (root / d).mkdir(parents=True)
