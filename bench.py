@@ -774,7 +774,8 @@ def main():
 
     from engine import workloads
     from engine.kernels.paged_attention import paged_attention_decode_batched
-    from engine.kernels.paged_attention_integration import paged_kv_write
+    from engine.kernels.paged_attention_integration import (paged_decode_kv_write_attention,
+                                                           paged_kv_write)
 
     dev = torch.device("cuda", 0)
     if args.library:
@@ -813,16 +814,22 @@ def main():
              if args.flush_mb > 0 else None)
 
     def step(i, ev=None):
+        """One decode layer's work: every sequence's new K/V row written to its slot, then
+        the batched attention. Without `ev`, as the decode step makes it
+        (paged_decode_kv_write_attention: the write launch also derives the attention
+        launch's schedule plan); with `ev`, as two calls with an event pair around the
+        attention call alone."""
         w = copies[i % len(copies)]
         if flush is not None:
             flush.fill_(i & 0xFF)
+        if ev is None:
+            return paged_decode_kv_write_attention(w.q, new_k, new_v, w.k_cache, w.v_cache,
+                                                   w.block_tables, w.seq_lens, w.scale)
         paged_kv_write(new_k, new_v, w.k_cache, w.v_cache, w.block_tables, w.seq_lens)
-        if ev is not None:
-            ev[0].record()
+        ev[0].record()
         out = paged_attention_decode_batched(w.q, w.k_cache, w.v_cache, w.block_tables,
                                              w.seq_lens, w.scale)
-        if ev is not None:
-            ev[1].record()
+        ev[1].record()
         return out
 
     for i in range(args.warmup):

@@ -55,7 +55,9 @@ enum {
  * removed, decode workspace sizes stated per current device; 10:
  * pa_decode_batched_noalloc_f16; 11: pa_decode_rope_batched_f16, decode workspace
  * with room for shared-prefix records; 12: pa_decode_batched_schedule; 13:
- * pa_decode_kv_write_batched_f16). */
+ * pa_decode_kv_write_batched_f16; 14: the decode workspace's head also holds the
+ * schedule plan that pa_decode_kv_write_batched_f16's write launch leaves for its
+ * attention launch, 8,448 bytes more). */
 PA_API int pa_abi_version(void);
 
 /* Message of the last failed call on this thread ("" after a success). */
@@ -113,7 +115,11 @@ PA_API int pa_decode_batched_f16(const void* q, const int64_t q_strides[3],
  * same bits) as pa_kv_write_f16 followed by pa_decode_batched_f16 on the same
  * stream. One launch where the batch takes one workgroup per (sequence,
  * kv-head group) pair at head_dim 64 or 128 and block size 16 or 32 (the
- * decode step's shapes); otherwise those two launches. Workspace: as for
+ * decode step's shapes); otherwise those two launches, and where the batch
+ * takes stream-K ranges at head_dim 64 or 128 and block size 16 or 32, the
+ * write launch also derives the attention launch's schedule plan once (from
+ * the same lengths and table rows) and leaves it in the workspace head, so
+ * that no attention workgroup derives it again. Workspace: as for
  * pa_decode_batched_f16 (pa_decode_batched_workspace_bytes). As for every
  * fused write here, a slot whose block id lies outside the pool is not
  * written, and the one-launch form then attends over the new rows where the
@@ -370,7 +376,7 @@ PA_API int pa_top2_f16(const void* logits, int64_t row_stride, int rows, int voc
  * scratch lives in a fixed array of PA_NOALLOC_SCRATCH_BYTES that the library
  * holds on each GPU it runs on until the process ends. One exception: where
  * the shared-prefix records of a stream-K launch would not fit the array
- * (head_dim 64: from 466 sequences at 2 kv heads, 117 at 8; in general
+ * (head_dim 64: from 465 sequences at 2 kv heads, 117 at 8; in general
  * 262144 + 2 x 256 x 4 x R + 2 x num_seqs x num_kv_heads x R > 16 MiB with R =
  * (32 + 16 x head_dim) x 4 bytes), the call reads shared prefixes once per
  * sequence instead: results within the attention tolerance of

@@ -49,7 +49,9 @@ def test_workspace_sizes():
     lib = _native.load()
     cus = _device_cus()
     rec = (32 + 16 * 64) * 4
-    counters = 65536 * 4  # per-pair arrival counters at the start of every decode workspace
+    # The head of every decode workspace: per-pair arrival counters, then the schedule plan a
+    # K/V write launch leaves for the attention launch after it (2 x 1024 + 64 ints).
+    counters = 65536 * 4 + (2 * 1024 + 64) * 4
 
     def streamk(seqs, kv_heads, grid, pair_heads, share):
         # Two record slots per workgroup of the grid; a slot holds one record per kv head of

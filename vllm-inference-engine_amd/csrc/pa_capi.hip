@@ -98,6 +98,67 @@ static int finish_launch(hipError_t e) {
   return PA_OK;
 }
 
+// Checks and fills the K/V write's arguments (the new rows [num_seqs, kv
+// heads, D] of key and value go to each sequence's slot of position L - 1);
+// `vec` tells whether every stride and base allows 16-byte copies. Returns a
+// PA_* status with the message set.
+static int kv_write_args(KVWriteArgs& a, bool& vec, const void* key, const int64_t key_strides[3],
+                         const void* value, const int64_t value_strides[3], void* k_cache,
+                         const int64_t k_strides[4], void* v_cache, const int64_t v_strides[4],
+                         const int32_t* block_tables, const int64_t bt_strides[2],
+                         const int32_t* seq_lens, int uniform_seq_len, int num_seqs,
+                         int num_kv_heads, int head_dim, int block_size, int num_blocks,
+                         int max_blocks_per_seq) {
+  if (!key || !value || !k_cache || !v_cache || !key_strides || !value_strides || !k_strides ||
+      !v_strides || !block_tables || !bt_strides) {
+    set_error("null pointer argument");
+    return PA_ERR_ARG;
+  }
+  if (num_kv_heads <= 0 || head_dim <= 0 || block_size <= 0 || num_blocks <= 0 ||
+      max_blocks_per_seq <= 0) {
+    set_error("num_kv_heads, head_dim, block_size, num_blocks and the table width must be "
+              "positive");
+    return PA_ERR_ARG;
+  }
+  if (k_strides[3] != 1 || v_strides[3] != 1) {
+    set_error("cache head_dim stride must be 1");
+    return PA_ERR_ARG;
+  }
+  a = KVWriteArgs{};
+  a.key = (const uint16_t*)key;
+  a.ks_b = key_strides[0];
+  a.ks_h = key_strides[1];
+  a.ks_d = key_strides[2];
+  a.val = (const uint16_t*)value;
+  a.vs_b = value_strides[0];
+  a.vs_h = value_strides[1];
+  a.vs_d = value_strides[2];
+  a.kc = (uint16_t*)k_cache;
+  a.kc_sb = k_strides[0];
+  a.kc_st = k_strides[1];
+  a.kc_sh = k_strides[2];
+  a.vc = (uint16_t*)v_cache;
+  a.vc_sb = v_strides[0];
+  a.vc_st = v_strides[1];
+  a.vc_sh = v_strides[2];
+  a.bt = block_tables;
+  a.bt_sb = bt_strides[0];
+  a.bt_sk = bt_strides[1];
+  a.lens = seq_lens;
+  a.uniform_len = uniform_seq_len;
+  a.num_seqs = num_seqs;
+  a.hkv = num_kv_heads;
+  a.D = head_dim;
+  a.bs = block_size;
+  a.num_blocks = num_blocks;
+  a.max_blocks = max_blocks_per_seq;
+  vec = head_dim % 8 == 0 && a.ks_d == 1 && a.vs_d == 1 && a.ks_b % 8 == 0 && a.ks_h % 8 == 0 &&
+        a.vs_b % 8 == 0 && a.vs_h % 8 == 0 && a.kc_sb % 8 == 0 && a.kc_st % 8 == 0 &&
+        a.kc_sh % 8 == 0 && a.vc_sb % 8 == 0 && a.vc_st % 8 == 0 && a.vc_sh % 8 == 0 &&
+        aligned(key, 16) && aligned(value, 16) && aligned(k_cache, 16) && aligned(v_cache, 16);
+  return PA_OK;
+}
+
 // ---- stream-K schedule: grid size and workspace layout ----
 
 static int device_cus();
@@ -324,7 +385,7 @@ using namespace pa;
 
 extern "C" {
 
-int pa_abi_version(void) { return 13; }
+int pa_abi_version(void) { return 14; }
 
 const char* pa_last_error(void) { return g_error.c_str(); }
 
@@ -558,8 +619,28 @@ int decode_batched(const void* q, const int64_t q_strides[3], const void* k_cach
       a.recs_bytes = rb < 0x7fffffffu ? (int)rb : 0x7fffffff;
       return finish_launch(launch_decode_write(a, *newrow, head_dim, (hipStream_t)stream));
     }
-    const int rc = write_first();
-    if (rc) return rc;
+    if (!plan_handover_supported(a, head_dim)) {
+      const int rc = write_first();
+      if (rc) return rc;
+    } else {
+      // Stream-K ranges: the K/V write launch also derives the plan once and
+      // leaves it in the workspace head for the attention launch, instead of
+      // every attention workgroup deriving it.
+      const int64_t ks[3] = {newrow->ks_b, newrow->ks_h, 1};
+      const int64_t vs[3] = {newrow->vs_b, newrow->vs_h, 1};
+      KVWriteArgs w;
+      bool vec = false;
+      int rc = kv_write_args(w, vec, newrow->key, ks, newrow->val, vs, const_cast<void*>(k_cache),
+                             k_strides, const_cast<void*>(v_cache), v_strides, block_tables,
+                             bt_strides, seq_lens, 0, num_seqs, num_kv_heads, head_dim,
+                             block_size, num_blocks, max_blocks_per_seq);
+      if (rc) return rc;
+      a.plan_out = (int*)((char*)workspace + kSkPairCounterBytes);
+      rc = finish_launch(launch_kv_write_plan(a, w, vec, (hipStream_t)stream));
+      if (rc) return rc;
+      a.plan_in = a.plan_out;
+      a.plan_out = nullptr;
+    }
   }
   return finish_launch(launch_streamk_planned(a, head_dim, workspace, workspace_bytes,
                                               (hipStream_t)stream));
@@ -702,54 +783,13 @@ int pa_kv_write_f16(const void* key, const int64_t key_strides[3], const void* v
     return PA_ERR_ARG;
   }
   if (num_seqs == 0) return PA_OK;
-  if (!key || !value || !k_cache || !v_cache || !key_strides || !value_strides || !k_strides ||
-      !v_strides || !block_tables || !bt_strides) {
-    set_error("null pointer argument");
-    return PA_ERR_ARG;
-  }
-  if (num_kv_heads <= 0 || head_dim <= 0 || block_size <= 0 || num_blocks <= 0 ||
-      max_blocks_per_seq <= 0) {
-    set_error("num_kv_heads, head_dim, block_size, num_blocks and the table width must be "
-              "positive");
-    return PA_ERR_ARG;
-  }
-  if (k_strides[3] != 1 || v_strides[3] != 1) {
-    set_error("cache head_dim stride must be 1");
-    return PA_ERR_ARG;
-  }
-  KVWriteArgs a{};
-  a.key = (const uint16_t*)key;
-  a.ks_b = key_strides[0];
-  a.ks_h = key_strides[1];
-  a.ks_d = key_strides[2];
-  a.val = (const uint16_t*)value;
-  a.vs_b = value_strides[0];
-  a.vs_h = value_strides[1];
-  a.vs_d = value_strides[2];
-  a.kc = (uint16_t*)k_cache;
-  a.kc_sb = k_strides[0];
-  a.kc_st = k_strides[1];
-  a.kc_sh = k_strides[2];
-  a.vc = (uint16_t*)v_cache;
-  a.vc_sb = v_strides[0];
-  a.vc_st = v_strides[1];
-  a.vc_sh = v_strides[2];
-  a.bt = block_tables;
-  a.bt_sb = bt_strides[0];
-  a.bt_sk = bt_strides[1];
-  a.lens = seq_lens;
-  a.uniform_len = uniform_seq_len;
-  a.num_seqs = num_seqs;
-  a.hkv = num_kv_heads;
-  a.D = head_dim;
-  a.bs = block_size;
-  a.num_blocks = num_blocks;
-  a.max_blocks = max_blocks_per_seq;
-  bool vec = head_dim % 8 == 0 && a.ks_d == 1 && a.vs_d == 1 && a.ks_b % 8 == 0 &&
-             a.ks_h % 8 == 0 && a.vs_b % 8 == 0 && a.vs_h % 8 == 0 && a.kc_sb % 8 == 0 &&
-             a.kc_st % 8 == 0 && a.kc_sh % 8 == 0 && a.vc_sb % 8 == 0 && a.vc_st % 8 == 0 &&
-             a.vc_sh % 8 == 0 && aligned(key, 16) && aligned(value, 16) && aligned(k_cache, 16) &&
-             aligned(v_cache, 16);
+  KVWriteArgs a;
+  bool vec = false;
+  const int rc = kv_write_args(a, vec, key, key_strides, value, value_strides, k_cache, k_strides,
+                               v_cache, v_strides, block_tables, bt_strides, seq_lens,
+                               uniform_seq_len, num_seqs, num_kv_heads, head_dim, block_size,
+                               num_blocks, max_blocks_per_seq);
+  if (rc) return rc;
   return finish_launch(launch_kv_write(a, vec, (hipStream_t)stream));
 }
 

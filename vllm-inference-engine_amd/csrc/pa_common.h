@@ -63,6 +63,11 @@ struct DecodeArgs {
   int share;
   int max_members;  // sequences per sharing group (at most kPfxMaxMembers)
   int slot_recs;    // records per partial-record slot: max(head_group, kPfxColBlocks) when sharing
+  // The stream-K plan (positions, then sharing information; layout of the
+  // workspace head) computed by the K/V write launch just before this one on
+  // the same stream, or null: every workgroup derives it.
+  const int* plan_in;
+  int* plan_out;  // where a K/V write launch leaves the plan
 };
 
 // Shared-prefix groups: leading table entries compared per sequence, most
@@ -84,7 +89,13 @@ __host__ __device__ constexpr int pfx_members(int g) {
 constexpr int kSkMaxSeqs = 1024;
 constexpr int kSkMaxWG = 1024;
 constexpr int kSkMaxPairs = 65536;
-constexpr size_t kSkCounterBytes = (size_t)kSkMaxPairs * sizeof(int);
+// Head of a stream-K workspace, ahead of the partial records: the pair
+// counters (zero between launches), then the plan a K/V write launch leaves
+// for the attention launch after it (each sequence's first list position,
+// kSkMaxSeqs + 1 ints, then its sharing information, kSkMaxSeqs ints).
+constexpr size_t kSkPairCounterBytes = (size_t)kSkMaxPairs * sizeof(int);
+constexpr size_t kSkPlanBytes = (size_t)(2 * kSkMaxSeqs + 64) * sizeof(int);
+constexpr size_t kSkCounterBytes = kSkPairCounterBytes + kSkPlanBytes;
 // Persistent workgroups per compute unit (each of eight wavefronts).
 constexpr int kSkWgPerCu = 1;
 
@@ -105,6 +116,42 @@ struct KVWriteArgs {
   int uniform_len;
   int num_seqs, hkv, D, bs, num_blocks, max_blocks;
 };
+
+// The K/V write's copies, items i0, i0 + step, ... of the num_seqs x hkv x
+// (D / 8 or D) list: sequence b's new key and value rows go to the slot of
+// position L - 1 (L = lens[b]), as 16-bit patterns (no float conversion), 16
+// bytes per item with VEC, one element otherwise. Sequences with no tokens,
+// a slot past the table or an out-of-range block id write nothing.
+template <bool VEC>
+__device__ inline void kv_write_rows(const KVWriteArgs& a, int64_t i0, int64_t step) {
+  const int per_row = VEC ? a.D / 8 : a.D;
+  const int64_t total = (int64_t)a.num_seqs * a.hkv * per_row;
+  for (int64_t i = i0; i < total; i += step) {
+    const int c = (int)(i % per_row);
+    const int64_t r = i / per_row;
+    const int h = (int)(r % a.hkv);
+    const int b = (int)(r / a.hkv);
+    const int L = a.lens ? a.lens[b] : a.uniform_len;
+    if (L <= 0) continue;
+    const int pos = L - 1;
+    const int lb = pos / a.bs;
+    if (lb >= a.max_blocks) continue;
+    const int id = a.bt[(int64_t)b * a.bt_sb + (int64_t)lb * a.bt_sk];
+    if (id < 0 || id >= a.num_blocks) continue;
+    const int off = pos - lb * a.bs;
+    const int64_t dk = (int64_t)id * a.kc_sb + (int64_t)off * a.kc_st + (int64_t)h * a.kc_sh;
+    const int64_t dv = (int64_t)id * a.vc_sb + (int64_t)off * a.vc_st + (int64_t)h * a.vc_sh;
+    const int64_t sk = (int64_t)b * a.ks_b + (int64_t)h * a.ks_h;
+    const int64_t sv = (int64_t)b * a.vs_b + (int64_t)h * a.vs_h;
+    if constexpr (VEC) {
+      *reinterpret_cast<uint4*>(a.kc + dk + c * 8) = *reinterpret_cast<const uint4*>(a.key + sk + c * 8);
+      *reinterpret_cast<uint4*>(a.vc + dv + c * 8) = *reinterpret_cast<const uint4*>(a.val + sv + c * 8);
+    } else {
+      a.kc[dk + c] = a.key[sk + c * a.ks_d];
+      a.vc[dv + c] = a.val[sv + c * a.vs_d];
+    }
+  }
+}
 
 // Argument bundle of the prefill block copy: source rows [num_tokens, Hkv, D]
 // with any element strides, written block by block into the caches.
@@ -257,6 +304,14 @@ hipError_t launch_decode_pair_rope(const DecodeArgs& a, const RopeIn& r, int D, 
 // launches (register spills in the segment walk).
 bool decode_write_supported(const DecodeArgs& a, int D);
 hipError_t launch_decode_write(const DecodeArgs& a, const RopeIn& r, int D, hipStream_t s);
+// The K/V write of `w` in one launch with the stream-K plan of the planned
+// launch `a` (written to a.plan_out), for an attention launch that follows it
+// on the same stream with a.plan_in set (launch_decode_streamk then runs the
+// kernel that reads the plan). Supported for stream-K ranges at head_dim 64 or
+// 128 and block size 16 or 32.
+bool plan_handover_supported(const DecodeArgs& a, int D);
+hipError_t launch_kv_write_plan(const DecodeArgs& a, const KVWriteArgs& w, bool vec,
+                                hipStream_t s);
 hipError_t launch_prefill_attn(const PrefillAttnArgs& a, int D, hipStream_t s);
 hipError_t launch_rmsnorm(const f16* x, int64_t xs, const f16* res, int64_t rs, f16* sum,
                           int64_t ss, const f16* w, f16* y, int64_t ys, int rows, int H,

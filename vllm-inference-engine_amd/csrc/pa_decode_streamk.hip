@@ -514,60 +514,28 @@ __device__ __forceinline__ void merge_waves(char* smem, int wave_bytes, int wave
   }
 }
 
-template <int D, int NT, int BS, int HG, int NW>
-__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
-void decode_streamk_kernel(DecodeArgs a) {
-  constexpr int NC = D / 32;
-  constexpr int ND = D / 16;
-  constexpr int LS = D + 8;
+// The stream-K plan: every sequence's first position in the list of work
+// items (prefix items, then pairs, with a segment cost per pair), into s_pos
+// (B + 1 entries), and with sharing its group information into s_info. Every
+// workgroup of a launch computes the same plan from the lengths and the
+// tables' leading columns; the decode layer's K/V write launch can compute it
+// once ahead of the attention launch instead. Runs in one workgroup of NW
+// wavefronts and ends with a barrier.
+template <int NW, bool SHARE>
+__device__ __forceinline__ void sk_plan(const DecodeArgs& a, const int NHG, int* s_pos,
+                                        int* s_info, int* s_wtot) {
   constexpr int NTHR = 64 * NW;
-  constexpr bool UNIFORM_TILE = BS > 0 && BS % 16 == 0;
-  // Prefix items are built where a tile lies in one block and four column
-  // blocks of accumulators fit the registers.
-  constexpr bool SHARE = UNIFORM_TILE && D <= 64;
-  constexpr int NCP = kPfxColBlocks;
-  constexpr int NTP = 2;  // tiles per chunk of a prefix item (one kv head)
-  constexpr int VST = NT * HG * 16 * LS;  // halves of one staging buffer (K or V) per wavefront
-  constexpr int CMB = 32 * HG + HG * ND * 64 * 4;  // floats of merge state per wavefront
-  constexpr int VSTP = SHARE ? NTP * 16 * LS : 0;
-  constexpr int CMBP = SHARE ? 32 * NCP + NCP * ND * 64 * 4 : 0;
-  // Per wavefront: a K and a V staging buffer; the merge state reuses the same
-  // bytes at segment ends.
-  constexpr int WAVE_BYTES_0 = 2 * VST * 2 > CMB * 4 ? 2 * VST * 2 : CMB * 4;
-  constexpr int WAVE_BYTES_1 = 2 * VSTP * 2 > CMBP * 4 ? 2 * VSTP * 2 : CMBP * 4;
-  constexpr int WAVE_BYTES = WAVE_BYTES_0 > WAVE_BYTES_1 ? WAVE_BYTES_0 : WAVE_BYTES_1;
   constexpr int PER = kSkMaxSeqs / NTHR;  // sequences planned per thread
-  constexpr int REC = record_floats(D);
   static_assert(PER * NTHR == kSkMaxSeqs, "plan layout");
-  __shared__ __attribute__((aligned(16))) char smem[NW * WAVE_BYTES];
-  // Sequence -> first list position of its items (prefix items, then pairs).
-  __shared__ int s_pos[kSkMaxSeqs + 1];
-  // Sequence -> its group's shared tiles (bits 0-7, zero: none), its member
-  // index (8-11) and the group's size (12-15).
-  __shared__ int s_info[SHARE ? kSkMaxSeqs : 1];
-  __shared__ int s_wtot[NW];
-  __shared__ int s_nmerge;                // pairs listed for merging
-  __shared__ int s_mlist[NTHR];           // pairs whose records this workgroup completed
-
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
-  const int row = lane & 15;
-  const int grp = lane >> 4;
   const int B = a.num_seqs;
   const int Hkv = a.hkv;
-  const int NHG = Hkv / HG;
-  const int bs = BS > 0 ? BS : a.bs;
-  const int G = gridDim.x;
+  const int bs = a.bs;
   const bool share = SHARE && a.share;
-  // List positions of a prefix item's tiles: one per tile. A prefix tile holds
-  // one kv head (a pair's tile HG of them), but a prefix wavefront keeps a
-  // chunk of NTP one-head tiles in flight where a pair's keeps NT tiles of HG
-  // heads, and its four column blocks cost more math per byte: in a
-  // bandwidth-saturated launch its bytes take about twice as long each.
+  // List positions of a prefix item's tiles: one per tile.
   auto pfx_pos = [&](int pt) { return pt; };
-
-  // ---- plan: lengths, sharing groups, the exclusive prefix of list positions ----
   // Every load of the plan is issued before any is used, so that the plan
   // costs one memory round trip: the table rows the sharing groups are found
   // from (below), then the lengths (unconditional, indices clamped; a branch
@@ -691,6 +659,76 @@ void decode_streamk_kernel(DecodeArgs a) {
     }
     if (tid == 0) s_pos[B] = total;
     __syncthreads();
+  }
+}
+
+// PLAN_IN: the plan comes from a.plan_in (left by the K/V write launch just
+// before this one) instead of being derived by every workgroup.
+template <int D, int NT, int BS, int HG, int NW, bool PLAN_IN = false>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void decode_streamk_kernel(DecodeArgs a) {
+  constexpr int NC = D / 32;
+  constexpr int ND = D / 16;
+  constexpr int LS = D + 8;
+  constexpr int NTHR = 64 * NW;
+  constexpr bool UNIFORM_TILE = BS > 0 && BS % 16 == 0;
+  // Prefix items are built where a tile lies in one block and four column
+  // blocks of accumulators fit the registers.
+  constexpr bool SHARE = UNIFORM_TILE && D <= 64;
+  constexpr int NCP = kPfxColBlocks;
+  constexpr int NTP = 2;  // tiles per chunk of a prefix item (one kv head)
+  constexpr int VST = NT * HG * 16 * LS;  // halves of one staging buffer (K or V) per wavefront
+  constexpr int CMB = 32 * HG + HG * ND * 64 * 4;  // floats of merge state per wavefront
+  constexpr int VSTP = SHARE ? NTP * 16 * LS : 0;
+  constexpr int CMBP = SHARE ? 32 * NCP + NCP * ND * 64 * 4 : 0;
+  // Per wavefront: a K and a V staging buffer; the merge state reuses the same
+  // bytes at segment ends.
+  constexpr int WAVE_BYTES_0 = 2 * VST * 2 > CMB * 4 ? 2 * VST * 2 : CMB * 4;
+  constexpr int WAVE_BYTES_1 = 2 * VSTP * 2 > CMBP * 4 ? 2 * VSTP * 2 : CMBP * 4;
+  constexpr int WAVE_BYTES = WAVE_BYTES_0 > WAVE_BYTES_1 ? WAVE_BYTES_0 : WAVE_BYTES_1;
+  constexpr int PER = kSkMaxSeqs / NTHR;  // sequences planned per thread
+  constexpr int REC = record_floats(D);
+  static_assert(PER * NTHR == kSkMaxSeqs, "plan layout");
+  __shared__ __attribute__((aligned(16))) char smem[NW * WAVE_BYTES];
+  // Sequence -> first list position of its items (prefix items, then pairs).
+  __shared__ int s_pos[kSkMaxSeqs + 1];
+  // Sequence -> its group's shared tiles (bits 0-7, zero: none), its member
+  // index (8-11) and the group's size (12-15).
+  __shared__ int s_info[SHARE ? kSkMaxSeqs : 1];
+  __shared__ int s_wtot[NW];
+  __shared__ int s_nmerge;                // pairs listed for merging
+  __shared__ int s_mlist[NTHR];           // pairs whose records this workgroup completed
+
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  const int row = lane & 15;
+  const int grp = lane >> 4;
+  const int B = a.num_seqs;
+  const int Hkv = a.hkv;
+  const int NHG = Hkv / HG;
+  const int bs = BS > 0 ? BS : a.bs;
+  const int G = gridDim.x;
+  const bool share = SHARE && a.share;
+  // List positions of a prefix item's tiles: one per tile. A prefix tile holds
+  // one kv head (a pair's tile HG of them), but a prefix wavefront keeps a
+  // chunk of NTP one-head tiles in flight where a pair's keeps NT tiles of HG
+  // heads, and its four column blocks cost more math per byte: in a
+  // bandwidth-saturated launch its bytes take about twice as long each.
+  auto pfx_pos = [&](int pt) { return pt; };
+
+  // ---- plan: lengths, sharing groups, the exclusive prefix of list positions ----
+  if constexpr (PLAN_IN) {
+    // Left by the K/V write launch just before this one on the stream (the
+    // same computation, run once instead of in every workgroup).
+    for (int i = tid; i <= B; i += NTHR) s_pos[i] = a.plan_in[i];
+    if constexpr (SHARE) {
+      if (share)
+        for (int i = tid; i < B; i += NTHR) s_info[i] = a.plan_in[kSkMaxSeqs + 1 + i];
+    }
+    __syncthreads();
+  } else {
+    sk_plan<NW, SHARE>(a, NHG, s_pos, s_info, s_wtot);
   }
 
   // Plan lookups for sequence b: shared tiles of its group, member index,
@@ -1407,6 +1445,13 @@ hipError_t launch_sk(const DecodeArgs& a, hipStream_t s) {
 }
 
 template <int D, int BS, int HG>
+hipError_t launch_sk_plan_in(const DecodeArgs& a, hipStream_t s) {
+  constexpr int NT = sk_chunk_tiles<D>(HG);
+  decode_streamk_kernel<D, NT, BS, HG, kSkWaves, true><<<a.num_wg, 64 * kSkWaves, 0, s>>>(a);
+  return hipGetLastError();
+}
+
+template <int D, int BS, int HG>
 hipError_t launch_pair_rope(const DecodeArgs& a, const RopeIn& r, hipStream_t s) {
   constexpr int NT = sk_chunk_tiles<D>(HG);
   decode_pair_kernel<D, NT, BS, HG, kSkWaves, 2><<<a.num_wg, 64 * kSkWaves, 0, s>>>(a, r);
@@ -1481,8 +1526,64 @@ hipError_t launch_decode_write(const DecodeArgs& a, const RopeIn& r, int D, hipS
   return a.bs == 16 ? launch_write<128, 16, 1>(a, r, s) : launch_write<128, 32, 1>(a, r, s);
 }
 
+// The decode layer's K/V write together with the stream-K plan of the
+// attention launch that follows it on the stream: workgroup 0 derives the
+// plan (the computation every attention workgroup would otherwise repeat)
+// and leaves it at a.plan_out; the other workgroups copy the new rows. The
+// attention launch starts once this one has ended, so it reads the plan and
+// the pool rows complete.
+template <int NW, bool VEC>
+__global__ __launch_bounds__(64 * NW) void kv_write_plan_kernel(DecodeArgs a, KVWriteArgs w) {
+  if (blockIdx.x == 0) {
+    __shared__ int s_pos[kSkMaxSeqs + 1];
+    __shared__ int s_info[kSkMaxSeqs];
+    __shared__ int s_wtot[NW];
+    sk_plan<NW, true>(a, a.hkv / a.head_group, s_pos, s_info, s_wtot);
+    for (int i = threadIdx.x; i <= a.num_seqs; i += 64 * NW) a.plan_out[i] = s_pos[i];
+    if (a.share)
+      for (int i = threadIdx.x; i < a.num_seqs; i += 64 * NW)
+        a.plan_out[kSkMaxSeqs + 1 + i] = s_info[i];
+    return;
+  }
+  kv_write_rows<VEC>(w, (int64_t)(blockIdx.x - 1) * blockDim.x + threadIdx.x,
+                     (int64_t)(gridDim.x - 1) * blockDim.x);
+}
+
+bool plan_handover_supported(const DecodeArgs& a, int D) {
+  return !a.pair_per_wg && a.num_seqs <= kSkMaxSeqs && (D == 64 || D == 128) &&
+         (a.bs == 16 || a.bs == 32) && tile_offsets_fit(a, D, a.head_group) &&
+         (a.head_group == 1 || D == 64);
+}
+
+hipError_t launch_decode_streamk_plan_in(const DecodeArgs& a, int D, hipStream_t s) {
+  if (!a.plan_in || !plan_handover_supported(a, D)) return hipErrorInvalidValue;
+  if (D == 64) {
+    if (a.head_group == 2)
+      return a.bs == 16 ? launch_sk_plan_in<64, 16, 2>(a, s) : launch_sk_plan_in<64, 32, 2>(a, s);
+    return a.bs == 16 ? launch_sk_plan_in<64, 16, 1>(a, s) : launch_sk_plan_in<64, 32, 1>(a, s);
+  }
+  return a.bs == 16 ? launch_sk_plan_in<128, 16, 1>(a, s) : launch_sk_plan_in<128, 32, 1>(a, s);
+}
+
+hipError_t launch_kv_write_plan(const DecodeArgs& a, const KVWriteArgs& w, bool vec,
+                                hipStream_t s) {
+  if (!a.plan_out || a.pair_per_wg || a.num_seqs > kSkMaxSeqs) return hipErrorInvalidValue;
+  constexpr int NTHR = 64 * kSkWaves;
+  const int per_row = vec ? w.D / 8 : w.D;
+  const int64_t total = (int64_t)w.num_seqs * w.hkv * per_row;
+  int64_t blocks = (total + NTHR - 1) / NTHR;
+  if (blocks < 1) blocks = 1;
+  if (blocks > 65535) blocks = 65535;
+  if (vec)
+    kv_write_plan_kernel<kSkWaves, true><<<(unsigned)blocks + 1, NTHR, 0, s>>>(a, w);
+  else
+    kv_write_plan_kernel<kSkWaves, false><<<(unsigned)blocks + 1, NTHR, 0, s>>>(a, w);
+  return hipGetLastError();
+}
+
 // Kv heads a wavefront handles together for this shape.
 hipError_t launch_decode_streamk(const DecodeArgs& a, int D, hipStream_t s) {
+  if (a.plan_in) return launch_decode_streamk_plan_in(a, D, s);
   const int hg = a.head_group;
   if (hg != 1 && !(hg == 2 && D <= 64 && a.hkv % 2 == 0)) return hipErrorInvalidValue;
   switch (D) {

@@ -14,34 +14,8 @@ namespace pa {
 
 template <bool VEC>
 __global__ __launch_bounds__(256) void kv_write_kernel(KVWriteArgs a) {
-  const int per_row = VEC ? a.D / 8 : a.D;
-  const int64_t total = (int64_t)a.num_seqs * a.hkv * per_row;
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
-       i += (int64_t)gridDim.x * blockDim.x) {
-    const int c = (int)(i % per_row);
-    const int64_t r = i / per_row;
-    const int h = (int)(r % a.hkv);
-    const int b = (int)(r / a.hkv);
-    const int L = a.lens ? a.lens[b] : a.uniform_len;
-    if (L <= 0) continue;
-    const int pos = L - 1;
-    const int lb = pos / a.bs;
-    if (lb >= a.max_blocks) continue;
-    const int id = a.bt[(int64_t)b * a.bt_sb + (int64_t)lb * a.bt_sk];
-    if (id < 0 || id >= a.num_blocks) continue;
-    const int off = pos - lb * a.bs;
-    const int64_t dk = (int64_t)id * a.kc_sb + (int64_t)off * a.kc_st + (int64_t)h * a.kc_sh;
-    const int64_t dv = (int64_t)id * a.vc_sb + (int64_t)off * a.vc_st + (int64_t)h * a.vc_sh;
-    const int64_t sk = (int64_t)b * a.ks_b + (int64_t)h * a.ks_h;
-    const int64_t sv = (int64_t)b * a.vs_b + (int64_t)h * a.vs_h;
-    if constexpr (VEC) {
-      *reinterpret_cast<uint4*>(a.kc + dk + c * 8) = *reinterpret_cast<const uint4*>(a.key + sk + c * 8);
-      *reinterpret_cast<uint4*>(a.vc + dv + c * 8) = *reinterpret_cast<const uint4*>(a.val + sv + c * 8);
-    } else {
-      a.kc[dk + c] = a.key[sk + c * a.ks_d];
-      a.vc[dv + c] = a.val[sv + c * a.vs_d];
-    }
-  }
+  kv_write_rows<VEC>(a, (int64_t)blockIdx.x * blockDim.x + threadIdx.x,
+                     (int64_t)gridDim.x * blockDim.x);
 }
 
 hipError_t launch_kv_write(const KVWriteArgs& a, bool vec, hipStream_t s) {

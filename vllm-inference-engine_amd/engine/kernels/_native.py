@@ -17,7 +17,7 @@ import torch  # noqa: F401  (must be loaded before the HIP library, see above)
 
 LIB_NAME = "libpa_gfx950.so"
 LIB_PATH = Path(__file__).with_name(LIB_NAME)
-ABI_VERSION = 13
+ABI_VERSION = 14
 
 PA_OK = 0
 PA_ERR_ARG = 1
