@@ -192,8 +192,8 @@ constexpr int kShareMinSeqs = 64;
 
 // Whether a launch over these sizes may build prefix items: head_dim <= 64,
 // block size 16 or 32, at least kShareMinSeqs sequences (and, at launch, pool
-// strides that the block-size-specialised kernels address; see
-// streamk_can_share).
+// strides that the block-size-specialised kernels address and table strides
+// the plan's 32-bit row offsets cover; see streamk_can_share).
 static bool streamk_may_share(int num_seqs, int head_dim, int block_size) {
   return num_seqs >= kShareMinSeqs && head_dim <= 64 && (block_size == 16 || block_size == 32);
 }

@@ -272,7 +272,8 @@ hipError_t launch_prefill_copy(const PrefillCopyArgs& a, bool vec, hipStream_t s
 hipError_t launch_rope_kv_write(const RopeKVArgs& a, bool vec, hipStream_t s);
 hipError_t launch_decode_streamk(const DecodeArgs& a, int D, hipStream_t s);
 // Whether the stream-K kernel launched for `a` builds prefix items (block size
-// 16 or 32, head_dim <= 64, pool strides its tile addressing covers).
+// 16 or 32, head_dim <= 64, pool strides its tile addressing covers, table
+// strides for which 32 rows and 64 columns span less than 2^31 entries).
 bool streamk_can_share(const DecodeArgs& a, int D);
 
 // The new token's rows of a fused decode-layer call (decode_pair_kernel with

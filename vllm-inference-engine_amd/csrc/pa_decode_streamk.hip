@@ -73,21 +73,41 @@ __host__ __device__ inline int64_t range_start(int w, int64_t T, int G) {
   return (int64_t)w * T / G;
 }
 
+// Inclusive prefix sum over the 64 lanes of a wavefront in DPP lane moves:
+// shifts by 1, 2, 4 and 8 within each row of 16 lanes (zero shifted in), then
+// each row's total broadcast to the rows after it (row_bcast 15 and 31).
+__device__ inline int wave_incl_scan(int x) {
+  x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xf, 0xf, false);  // row_shr:1
+  x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xf, 0xf, false);  // row_shr:2
+  x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xf, 0xf, false);  // row_shr:4
+  x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xf, 0xf, false);  // row_shr:8
+  x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xa, 0xf, false);  // row_bcast:15 (rows 1, 3)
+  x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xc, 0xf, false);  // row_bcast:31 (rows 2, 3)
+  return x;
+}
+
 // Exclusive prefix sums over a workgroup of NW wavefronts, PER values per
 // thread (thread t holds entries t * PER .. t * PER + PER - 1); returns the
-// total. s_tot holds NW ints; the call starts and ends with a barrier.
-template <int PER, int NW>
+// total. s_tot holds NW ints, written once per call with one barrier: a
+// second call reusing s_tot needs a barrier before it. The wavefront scan is
+// DPP lane moves with DPP, else six lane shuffles (through LDS): the DPP form
+// is shorter, but in some kernels it costs registers their streaming loop
+// needs (one more wavefront spill at one kv head per pair, head_dim 64).
+template <int PER, int NW, bool DPP>
 __device__ inline int block_excl_sum(int (&v)[PER], int* s_tot, int lane, int wave) {
   int local = 0;
 #pragma unroll
   for (int i = 0; i < PER; ++i) local += v[i];
   int incl = local;
+  if constexpr (DPP) {
+    incl = wave_incl_scan(local);
+  } else {
 #pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const int y = __shfl_up(incl, off);
-    if (lane >= off) incl += y;
+    for (int off = 1; off < 64; off <<= 1) {
+      const int y = __shfl_up(incl, off);
+      if (lane >= off) incl += y;
+    }
   }
-  __syncthreads();
   if (lane == 63) s_tot[wave] = incl;
   __syncthreads();
   int run = incl - local, total = 0;
@@ -102,7 +122,6 @@ __device__ inline int block_excl_sum(int (&v)[PER], int* s_tot, int lane, int wa
     v[i] = run;
     run += t;
   }
-  __syncthreads();
   return total;
 }
 
@@ -521,7 +540,7 @@ __device__ __forceinline__ void merge_waves(char* smem, int wave_bytes, int wave
 // tables' leading columns; the decode layer's K/V write launch can compute it
 // once ahead of the attention launch instead. Runs in one workgroup of NW
 // wavefronts and ends with a barrier.
-template <int NW, bool SHARE>
+template <int NW, bool SHARE, bool DPP_SCAN>
 __device__ __forceinline__ void sk_plan(const DecodeArgs& a, const int NHG, int* s_pos,
                                         int* s_info, int* s_wtot) {
   constexpr int NTHR = 64 * NW;
@@ -543,12 +562,17 @@ __device__ __forceinline__ void sk_plan(const DecodeArgs& a, const int NHG, int*
   int rows[32];
   const int capc = min(kPfxCapBlocks, a.max_blocks);
   const int col = min(lane, capc - 1);
+  // Rows b0 .. b0 + 31 (clamped to the batch): 32-bit offsets from the
+  // slice's first row (the host enables sharing only where 32 rows and 64
+  // columns of the table span less than 2^31 entries), so a row costs a min
+  // and a 32-bit multiply instead of a 64-bit product.
   auto load_rows = [&](int b0) {
+    const int32_t* base = a.bt + (int64_t)b0 * a.bt_sb;
+    const int rlast = B - 1 - b0;
+    const uint32_t cofs = (uint32_t)col * (uint32_t)a.bt_sk;
 #pragma unroll
-    for (int r = 0; r < 32; ++r) {
-      const int rb = min(b0 + r, B - 1);
-      rows[r] = a.bt[(int64_t)rb * a.bt_sb + (int64_t)col * a.bt_sk];
-    }
+    for (int r = 0; r < 32; ++r)
+      rows[r] = base[(uint32_t)min(r, rlast) * (uint32_t)a.bt_sb + cofs];
   };
   // The sharing compare also needs lane r's length of sequence b0 + r.
   int wlen = 0;
@@ -593,17 +617,34 @@ __device__ __forceinline__ void sk_plan(const DecodeArgs& a, const int NHG, int*
         const int limv = min(capc, min(fl, __shfl_up(fl, 1)));
         // ct: lane i < 32 gets the tiles sequence b0 + i shares with b0 + i - 1
         // (zero for the slice's first sequence: groups start at slice starts).
-        // Per sequence one compare into a 64-bit lane mask; the first mismatch
-        // or limit is found in scalar registers and written into lane r.
-        int ct = 0;
+        // Per sequence one compare into a 64-bit lane mask; its first set bit
+        // (the first differing entry, 64 if none) is found in scalar registers,
+        // parked in the slice's own s_info entries (overwritten below by this
+        // wavefront), read back by lane r and capped at the lane's limit. The
+        // 31 compares are independent; capping each in scalar registers and
+        // writing it into lane r through inline assembly (a scheduling barrier
+        // to the compiler) chained them one after another: about 1.5 us per
+        // slice.
+        // In four chunks of eight, so that at most eight results are live in
+        // scalar registers at once.
 #pragma unroll
-        for (int r = 1; r < 32; ++r) {
-          const int lim = __builtin_amdgcn_readlane(limv, r);
-          const uint64_t diff = __ballot(rows[r] != rows[r - 1]) | (lim >= 64 ? 0ull : ~0ull << lim);
-          const int c = diff ? (int)__builtin_ctzll(diff) : 64;
-          const int v = min(c * (bs / 16), 255);
-          asm volatile("v_writelane_b32 %0, %1, %2" : "+v"(ct) : "s"(v), "i"(r));
+        for (int r0 = 0; r0 < 32; r0 += 8) {
+          int cr[8];
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            const int r = r0 + i;
+            const uint64_t diff = r == 0 ? 0 : __ballot(rows[r] != rows[r > 0 ? r - 1 : 0]);
+            cr[i] = diff ? (int)__builtin_ctzll(diff) : 64;
+          }
+          if (lane == 0) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) s_info[b0 + r0 + i] = cr[i];
+          }
         }
+        wave_lds_fence();
+        const int cfirst = lane >= 1 && lane < 32 ? s_info[b0 + lane] : 64;
+        wave_lds_fence();
+        int ct = lane >= 1 && lane < 32 ? min(min(cfirst, limv) * (bs / 16), 255) : 0;
         const int bl = b0 + lane;  // lane i < 32: sequence b0 + i
         const bool valid = lane < 32 && bl < B;
         if (!valid) ct = 0;
@@ -651,7 +692,7 @@ __device__ __forceinline__ void sk_plan(const DecodeArgs& a, const int NHG, int*
       const int w = n - pt > 0 ? n - pt + a.seg_cost : 0;
       cnt[i] = b < B ? NHG * w + (pt > 0 && m == 0 ? Hkv * (pfx_pos(pt) + a.seg_cost) : 0) : 0;
     }
-    const int total = block_excl_sum<PER, NW>(cnt, s_wtot, lane, wave);
+    const int total = block_excl_sum<PER, NW, DPP_SCAN>(cnt, s_wtot, lane, wave);
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
       const int b = tid * PER + i;
@@ -728,7 +769,7 @@ void decode_streamk_kernel(DecodeArgs a) {
     }
     __syncthreads();
   } else {
-    sk_plan<NW, SHARE>(a, NHG, s_pos, s_info, s_wtot);
+    sk_plan<NW, SHARE, HG == 2>(a, NHG, s_pos, s_info, s_wtot);
   }
 
   // Plan lookups for sequence b: shared tiles of its group, member index,
@@ -1493,7 +1534,12 @@ hipError_t launch_sk_bs(const DecodeArgs& a, hipStream_t s) {
 // Whether the kernel launched for these arguments builds prefix items (the
 // host sizes the workspace and sets a.share only then).
 bool streamk_can_share(const DecodeArgs& a, int D) {
-  return D <= 64 && (a.bs == 16 || a.bs == 32) && tile_offsets_fit(a, D, a.head_group);
+  // The plan reads 32 rows and kPfxCapBlocks columns of the table per slice
+  // with 32-bit offsets.
+  const bool table_fits = a.bt_sb >= 0 && a.bt_sk >= 0 &&
+                          a.bt_sb * 31 + a.bt_sk * (kPfxCapBlocks - 1) < ((int64_t)1 << 31);
+  return D <= 64 && (a.bs == 16 || a.bs == 32) && tile_offsets_fit(a, D, a.head_group) &&
+         table_fits;
 }
 
 bool pair_rope_supported(const DecodeArgs& a, int D) {
@@ -1538,7 +1584,7 @@ __global__ __launch_bounds__(64 * NW) void kv_write_plan_kernel(DecodeArgs a, KV
     __shared__ int s_pos[kSkMaxSeqs + 1];
     __shared__ int s_info[kSkMaxSeqs];
     __shared__ int s_wtot[NW];
-    sk_plan<NW, true>(a, a.hkv / a.head_group, s_pos, s_info, s_wtot);
+    sk_plan<NW, true, true>(a, a.hkv / a.head_group, s_pos, s_info, s_wtot);
     for (int i = threadIdx.x; i <= a.num_seqs; i += 64 * NW) a.plan_out[i] = s_pos[i];
     if (a.share)
       for (int i = threadIdx.x; i < a.num_seqs; i += 64 * NW)
