@@ -168,6 +168,25 @@ def test_single_sequence_long_prefix_split(cuda_device):
         assert torch.equal(run(c, 0.125), out)
 
 
+@pytest.mark.parametrize("d", [64, 32])
+def test_both_wavefront_forms(cuda_device, d):
+    """Up to head_dim 64 a block of 128 columns runs as four wavefronts of two column groups
+    when the launch is not split and the new tokens are at most half the table's positions,
+    else as eight wavefronts of one group. A larger max_query_len (still a valid bound) selects
+    the second form for the same inputs; both match the oracle and each other."""
+    c = build(14, 2, d, 16, [1536] * 8, [512] * 8, seed=25 + d, device=cuda_device)
+    scale = d ** -0.5
+    four = run(c, scale)  # 448 workgroups, no split, 2 x 512 <= 1536
+    eight = paged_attention_prefill(c["qd"], c["kd"], c["vd"], c["btd"], c["lensd"], c["qsld"],
+                                    1024, scale)  # 2 x 1024 > 1536: 896 workgroups, half empty
+    want = oracle(c, scale)
+    e4, e8 = max_err(four, want), max_err(eight, want)
+    print(f"[prefill] d={d} four-wavefront max_err={e4:.2e} eight-wavefront {e8:.2e}", flush=True)
+    assert e4 <= TOL and e8 <= TOL
+    assert (four.float() - eight.float()).abs().max().item() <= TOL
+    assert torch.equal(run(c, scale), four)
+
+
 def test_split_counters_return_to_zero(cuda_device):
     c = build(28, 4, 128, 16, [3000, 10], [700, 10], seed=19, device=cuda_device)
     run(c, 128 ** -0.5)

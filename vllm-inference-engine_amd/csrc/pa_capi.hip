@@ -328,7 +328,7 @@ constexpr int kPrefillMinSplitTiles = 4;
 
 struct PrefillPlan {
   int64_t col_blocks = 0, split_tiles = 1, max_splits = 1;
-  int col_groups = 1;
+  int col_groups = 1, wave_groups = 1;
   size_t counter_bytes = 0, ws_bytes = 0;
 };
 
@@ -371,6 +371,23 @@ static PrefillPlan prefill_plan(int num_seqs, int num_q_heads, int num_kv_heads,
     p.split_tiles = st;
     p.max_splits = (max_tiles + st - 1) / st;
   }
+  // Up to head_dim 64, 128 columns run as four wavefronts of two column groups
+  // (each LDS operand read feeds two MFMAs; two wavefronts per SIMD) or eight of
+  // one group (four per SIMD). With workgroups of even length the first is
+  // faster; where some finish early (the causal part is most of the context, or
+  // the last piece of a split key range is short) a workgroup left alone on a CU
+  // has one wavefront per SIMD in that form and the second is faster. Measured on
+  // MI355X at g = 7, block 16 (back-to-back means of 30 calls, three alternating
+  // rounds on one box): head_dim 64, 8 x (2048 + 512)
+  // 52.6-53.4 vs 55.8-56.2 us, 4 x (8192 + 1024) 177.0-177.8 vs 187.3-188.7,
+  // 8 x (2048 + 1024) 109.4-110.2 vs 114.4-114.8; 2 x 2048-token prompts 35.3-35.4
+  // vs 34.1-34.2, 8192 + 1024 split four ways 66.8-67.3 vs 62.7-63.5; head_dim 32,
+  // 8 x (2048 + 512) 39.3-40.4 vs 40.0-42.2.
+  if (head_dim > 64)
+    p.wave_groups = p.col_groups;
+  else if (p.col_groups == 2 && p.max_splits == 1 &&
+           2 * (int64_t)max_query_len <= (int64_t)max_blocks * block_size)
+    p.wave_groups = 2;
   if (p.max_splits > 1) {
     p.counter_bytes = kPfCounterBytes;
     p.ws_bytes = p.counter_bytes +
@@ -1167,6 +1184,7 @@ int pa_prefill_attention_f16(const void* q, const int64_t q_strides[3], const vo
   a.max_blocks = max_blocks_per_seq;
   a.col_blocks = (int)plan.col_blocks;
   a.col_groups = plan.col_groups;
+  a.wave_groups = plan.wave_groups;
   a.scale_log2 = scale * kLog2e;
   a.split_tiles = (int)plan.split_tiles;
   a.max_splits = (int)plan.max_splits;

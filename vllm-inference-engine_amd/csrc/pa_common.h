@@ -214,7 +214,8 @@ struct PrefillAttnArgs {
   int64_t o_st, o_sh;
   int num_seqs, num_tokens, hkv, g, bs, num_blocks, max_blocks;
   int col_blocks;  // column blocks per (sequence, kv head): ceil(max_query_len * g / columns)
-  int col_groups;  // column groups of 16 per wavefront (columns per workgroup = 64 x this)
+  int col_groups;   // columns per workgroup in units of 64: 1 or 2
+  int wave_groups;  // column groups of 16 per wavefront: 1, or 2 (half the wavefronts)
   float scale_log2;
   // Key-range split: a column block whose keys span more than split_tiles key
   // tiles is processed by several workgroups (up to max_splits), which leave
@@ -225,11 +226,11 @@ struct PrefillAttnArgs {
 };
 
 // Columns of a prefill workgroup in units of 64 (token, query head) columns:
-// two (128 columns) below head_dim 256, where the registers allow it; the
-// kernel runs them as eight wavefronts of one group of 16 up to head_dim 64,
-// four wavefronts of two groups at head_dim 128 (each K and V operand read
-// from LDS then feeds two MFMAs). Launches with few column blocks take one
-// unit instead (twice the workgroups); see prefill_plan.
+// two (128 columns) below head_dim 256, where the registers allow it. At head_dim
+// 128 the kernel runs them as four wavefronts of two groups of 16 (each K and V
+// operand read from LDS then feeds two MFMAs); up to head_dim 64 as either that
+// or eight wavefronts of one group, chosen per launch by prefill_plan. Launches
+// with few column blocks take one unit instead (twice the workgroups).
 __host__ __device__ constexpr int prefill_col_groups(int D) { return D <= 128 ? 2 : 1; }
 // The prefill workspace starts with a fixed region of arrival counters, one per
 // column block of a split launch, so that the counters of every launch sit at

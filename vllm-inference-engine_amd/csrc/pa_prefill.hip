@@ -7,11 +7,11 @@
 //
 // Work split. The (token, query head) pairs of one sequence and one kv head
 // form a list of n * g columns, token-major. A workgroup takes 128
-// consecutive columns (eight wavefronts of one group of 16 columns up to
-// head_dim 64, four wavefronts of two groups at head_dim 128, where each K or V
-// operand read from LDS feeds two MFMAs; 64 columns, one group per wavefront,
-// at head_dim 256), so the K/V rows it stages serve all g query heads of the
-// kv head at once. Workgroups with the latest columns see the most keys; they
+// consecutive columns (four wavefronts of two groups of 16 columns, where each
+// K or V operand read from LDS feeds two MFMAs, or up to head_dim 64 eight
+// wavefronts of one group; 64 columns, one group per wavefront, at head_dim
+// 256), so the K/V rows it stages serve all g query heads of the kv head at
+// once. Workgroups with the latest columns see the most keys; they
 // are numbered first so the longest runs start first.
 //
 // Per key tile (128 keys up to head_dim 64, else 64) the workgroup loads K
@@ -483,26 +483,30 @@ __global__ __launch_bounds__(64 * NW) void prefill_attn_kernel(PrefillAttnArgs a
 }
 
 // A column block of 64 CG columns runs as four wavefronts of CG groups of 16
-// columns; up to head_dim 64, a block of two groups per wavefront runs as
-// eight wavefronts of one group instead: the same columns and the same
-// arithmetic per column (the same result bits), four wavefronts per SIMD
-// instead of two (117 VGPRs instead of 218 at head_dim 64). Measured on MI355X
-// (HIP events, means of 30 calls, A/B on one box): one sequence of 8192 cached
-// + 1024 new tokens (split key ranges) 73.9-76.5 vs 78.8-78.9 us; 4 x (2048 +
-// 512) at head_dim 32 33.2-33.4 vs 33.9-34.1 us; 8 x (2048 + 512) at head_dim
-// 64 unchanged (68.7-69.7 vs 68.9). At head_dim 128 the eight-wavefront form
-// would hold one workgroup per CU (148 VGPRs), so four wavefronts stay.
+// columns; up to head_dim 64, a block of two groups per wavefront may run as
+// eight wavefronts of one group instead (a.wave_groups, chosen by the host):
+// four wavefronts per SIMD instead of two (125 VGPRs instead of 230 at head_dim
+// 64). Each column's arithmetic is the same except where a wavefront raises its
+// running maxima: it does so for all the columns it holds at once (16 or 32),
+// so the two forms agree to rounding and mostly bit for bit. At head_dim 128 the eight-wavefront form would hold one workgroup per CU
+// (148 VGPRs), so four wavefronts stay.
+template <int D, int BS, int CG>
+static hipError_t launch_prefill_bs(const PrefillAttnArgs& a, int64_t grid, hipStream_t s) {
+  if constexpr (D <= 64 && CG == 2) {
+    if (a.wave_groups == 1) {
+      hipLaunchKernelGGL((prefill_attn_kernel<D, BS, 1, 8>), dim3((unsigned)grid), dim3(512), 0, s, a);
+      return hipGetLastError();
+    }
+  }
+  if (a.wave_groups != CG) return hipErrorInvalidValue;
+  hipLaunchKernelGGL((prefill_attn_kernel<D, BS, CG, 4>), dim3((unsigned)grid), dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
 template <int D, int CG>
 static hipError_t launch_prefill_dc(const PrefillAttnArgs& a, hipStream_t s) {
   const int64_t grid = (int64_t)a.col_blocks * a.max_splits * a.num_seqs * a.hkv;
-  constexpr bool kEight = D <= 64 && CG == 2;
-  constexpr int CGK = kEight ? 1 : CG;
-  constexpr int NW = kEight ? 8 : 4;
-  if (a.bs == 16)
-    hipLaunchKernelGGL((prefill_attn_kernel<D, 16, CGK, NW>), dim3((unsigned)grid), dim3(64 * NW), 0, s, a);
-  else
-    hipLaunchKernelGGL((prefill_attn_kernel<D, 0, CGK, NW>), dim3((unsigned)grid), dim3(64 * NW), 0, s, a);
-  return hipGetLastError();
+  return a.bs == 16 ? launch_prefill_bs<D, 16, CG>(a, grid, s) : launch_prefill_bs<D, 0, CG>(a, grid, s);
 }
 
 template <int D>
