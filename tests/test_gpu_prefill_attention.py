@@ -168,20 +168,26 @@ def test_single_sequence_long_prefix_split(cuda_device):
         assert torch.equal(run(c, 0.125), out)
 
 
-@pytest.mark.parametrize("d", [64, 32])
-def test_both_wavefront_forms(cuda_device, d):
+@pytest.mark.parametrize("d,bs,ragged", [(64, 16, False), (32, 16, False), (64, 32, True),
+                                         (64, 8, True), (32, 32, True)])
+def test_both_wavefront_forms(cuda_device, d, bs, ragged):
     """Up to head_dim 64 a block of 128 columns runs as four wavefronts of two column groups
     when the launch is not split and the new tokens are at most half the table's positions,
     else as eight wavefronts of one group. A larger max_query_len (still a valid bound) selects
-    the second form for the same inputs; both match the oracle and each other."""
-    c = build(14, 2, d, 16, [1536] * 8, [512] * 8, seed=25 + d, device=cuda_device)
+    the second form for the same inputs; both match the oracle and each other. Block 16 takes
+    the kernels specialised for it, the other sizes the general ones; ragged batches leave
+    some column blocks empty and cut others short."""
+    ctx = [1536, 1500, 1400, 1536, 1300, 1536, 1536, 1200] if ragged else [1536] * 8
+    new = [512, 300, 512, 450, 512, 17, 512, 512] if ragged else [512] * 8
+    c = build(14, 2, d, bs, ctx, new, seed=25 + d + bs, device=cuda_device)
     scale = d ** -0.5
     four = run(c, scale)  # 448 workgroups, no split, 2 x 512 <= 1536
     eight = paged_attention_prefill(c["qd"], c["kd"], c["vd"], c["btd"], c["lensd"], c["qsld"],
                                     1024, scale)  # 2 x 1024 > 1536: 896 workgroups, half empty
     want = oracle(c, scale)
     e4, e8 = max_err(four, want), max_err(eight, want)
-    print(f"[prefill] d={d} four-wavefront max_err={e4:.2e} eight-wavefront {e8:.2e}", flush=True)
+    print(f"[prefill] d={d} bs={bs} ragged={ragged} four-wavefront max_err={e4:.2e} "
+          f"eight-wavefront {e8:.2e}", flush=True)
     assert e4 <= TOL and e8 <= TOL
     assert (four.float() - eight.float()).abs().max().item() <= TOL
     assert torch.equal(run(c, scale), four)
