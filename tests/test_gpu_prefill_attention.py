@@ -193,6 +193,23 @@ def test_both_wavefront_forms(cuda_device, d, bs, ragged):
     assert torch.equal(run(c, scale), four)
 
 
+def test_long_split_pieces_four_wavefronts(cuda_device):
+    """At head_dim 64, key ranges split into pieces of 48 tiles or more run as four wavefronts
+    of two column groups (192 column blocks split two ways, 48 tiles each); a larger
+    max_query_len gives 384 blocks and no split. Both match the oracle and each other."""
+    c = build(16, 8, 64, 16, [12288, 4000, 12000], [512, 512, 300], seed=31, device=cuda_device)
+    split = run(c, 0.125)
+    whole = paged_attention_prefill(c["qd"], c["kd"], c["vd"], c["btd"], c["lensd"], c["qsld"],
+                                    1024, 0.125)
+    want = oracle(c, 0.125)
+    es, ew = max_err(split, want), max_err(whole, want)
+    print(f"[prefill] long split pieces max_err={es:.2e}, unsplit {ew:.2e}", flush=True)
+    assert es <= TOL and ew <= TOL
+    assert (split.float() - whole.float()).abs().max().item() <= TOL
+    for _ in range(2):
+        assert torch.equal(run(c, 0.125), split)
+
+
 def test_split_counters_return_to_zero(cuda_device):
     c = build(28, 4, 128, 16, [3000, 10], [700, 10], seed=19, device=cuda_device)
     run(c, 128 ** -0.5)

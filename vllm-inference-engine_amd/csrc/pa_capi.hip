@@ -376,17 +376,24 @@ static PrefillPlan prefill_plan(int num_seqs, int num_q_heads, int num_kv_heads,
   // one group (four per SIMD). With workgroups of even length the first is
   // faster; where some finish early (the causal part is most of the context, or
   // the last piece of a split key range is short) a workgroup left alone on a CU
-  // has one wavefront per SIMD in that form and the second is faster. Measured on
-  // MI355X at g = 7, block 16 (back-to-back means of 30 calls, three alternating
-  // rounds on one box): head_dim 64, 8 x (2048 + 512)
-  // 52.6-53.4 vs 55.8-56.2 us, 4 x (8192 + 1024) 177.0-177.8 vs 187.3-188.7,
-  // 8 x (2048 + 1024) 109.4-110.2 vs 114.4-114.8; 2 x 2048-token prompts 35.3-35.4
-  // vs 34.1-34.2, 8192 + 1024 split four ways 66.8-67.3 vs 62.7-63.5; head_dim 32,
-  // 8 x (2048 + 512) 39.3-40.4 vs 40.0-42.2.
+  // has one wavefront per SIMD in that form and the second is faster. At head_dim
+  // 64 split pieces of 48 tiles and more are long enough for the first. Measured
+  // on MI355X at g = 7, block 16 (back-to-back means of 30 calls, three
+  // alternating rounds on one box): head_dim 64, 8 x (2048 + 512) 52.6-53.4 vs
+  // 55.8-56.2 us, 4 x (8192 + 1024) 177.0-177.8 vs 187.3-188.7, 8 x (2048 +
+  // 1024) 109.4-110.2 vs 114.4-114.8; 2 x 2048-token prompts 35.3-35.4 vs
+  // 34.1-34.2, 8192 + 1024 split four ways (pieces of 18 tiles) 66.6-67.3 vs
+  // 62.7-63.5; split two ways: 16384 + 2048 190.4-193.8 vs 199.2-201.3, 32768 +
+  // 2048 344.9-346.6 vs 362.7-366.7, 12288 + 2048 151.7-152.4 vs 156.7-158.9;
+  // 16384 + 1024 split four ways (34 tiles) 104.5-105.4 vs 104.8-105.2; head_dim
+  // 32, 8 x (2048 + 512) 39.3-40.4 vs 40.0-42.2, 16384 + 2048 split two ways
+  // 136.9-137.6 vs 134.7-135.6.
+  constexpr int64_t kPrefillLongPieceTiles = 48;
   if (head_dim > 64)
     p.wave_groups = p.col_groups;
-  else if (p.col_groups == 2 && p.max_splits == 1 &&
-           2 * (int64_t)max_query_len <= (int64_t)max_blocks * block_size)
+  else if (p.col_groups == 2 &&
+           ((p.max_splits == 1 && 2 * (int64_t)max_query_len <= (int64_t)max_blocks * block_size) ||
+            (p.max_splits > 1 && head_dim == 64 && p.split_tiles >= kPrefillLongPieceTiles)))
     p.wave_groups = 2;
   if (p.max_splits > 1) {
     p.counter_bytes = kPfCounterBytes;
