@@ -488,8 +488,9 @@ __global__ __launch_bounds__(64 * NW) void prefill_attn_kernel(PrefillAttnArgs a
 // four wavefronts per SIMD instead of two (125 VGPRs instead of 230 at head_dim
 // 64). Each column's arithmetic is the same except where a wavefront raises its
 // running maxima: it does so for all the columns it holds at once (16 or 32),
-// so the two forms agree to rounding and mostly bit for bit. At head_dim 128 the eight-wavefront form would hold one workgroup per CU
-// (148 VGPRs), so four wavefronts stay.
+// so the two forms agree to rounding and mostly bit for bit. At head_dim 128
+// the eight-wavefront form would hold one workgroup per CU (148 VGPRs), so four
+// wavefronts stay.
 template <int D, int BS, int CG>
 static hipError_t launch_prefill_bs(const PrefillAttnArgs& a, int64_t grid, hipStream_t s) {
   if constexpr (D <= 64 && CG == 2) {
